@@ -1,0 +1,121 @@
+"""ctypes binding of libaffmae.so (the C ABI in include/affmae.h).
+
+The library is loaded after torch so that it binds to the HIP runtime torch
+already loaded (both use the soname libamdhip64.so.7); stream handles from
+``torch.cuda.current_stream().cuda_stream`` are therefore valid here.  There
+is no CPU fallback: every op raises if the library or a GPU is missing.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libaffmae.so"
+
+AFF_OK = 0
+AFF_ERR_INVALID_ARG = 1
+AFF_ERR_UNSUPPORTED = 2
+AFF_ERR_WORKSPACE = 3
+AFF_ERR_LAUNCH = 4
+
+AFF_F32, AFF_F16, AFF_BF16 = 0, 1, 2
+DTYPE_CODE = {torch.float32: AFF_F32, torch.float16: AFF_F16, torch.bfloat16: AFF_BF16}
+
+ABI_VERSION = 2
+
+P = ctypes.c_void_p
+I32 = ctypes.c_int
+I64 = ctypes.c_int64
+F32 = ctypes.c_float
+SZ = ctypes.c_size_t
+
+
+class NbhdAttnArgs(ctypes.Structure):
+    """Mirror of ``aff_nbhd_attn_args`` (include/affmae.h)."""
+    _fields_ = [
+        ("dtype", I32), ("B", I32), ("H", I32), ("N", I32), ("M", I32), ("D", I32),
+        ("scale", F32),
+        ("q", P), ("q_sb", I64), ("q_sh", I64), ("q_sn", I64),
+        ("k", P), ("k_sb", I64), ("k_sh", I64), ("k_sn", I64),
+        ("v", P), ("v_sb", I64), ("v_sh", I64), ("v_sn", I64),
+        ("member_idx", P), ("idx_is_i64", I32), ("mi_sb", I64), ("mi_sn", I64),
+        ("bias_mode", I32),
+        ("bias", P), ("bias_dtype", I32), ("bias_sb", I64), ("bias_sh", I64), ("bias_sn", I64),
+        ("pe_idx", P), ("pe_is_i64", I32), ("pe_sb", I64), ("pe_sn", I64),
+        ("table", P), ("table_dtype", I32), ("table_rows", I64),
+        ("pos", P), ("pos_sb", I64), ("pos_sn", I64),
+        ("rel_width", I32),
+        ("pos_w", P), ("pos_b", P),
+        ("mask", P), ("mask_sb", I64), ("mask_sh", I64), ("mask_sn", I64),
+        ("blank_k", P), ("blank_v", P),
+        ("out", P), ("o_sb", I64), ("o_sh", I64), ("o_sn", I64),
+        ("lse", P),
+    ]
+
+
+# Every symbol include/affmae.h declares, with (restype, argtypes).
+SIGNATURES = {
+    "aff_last_error": (ctypes.c_char_p, []),
+    "aff_abi_version": (I32, []),
+    "aff_knn_workspace_bytes": (SZ, [I32, I32, I32, I32, I32]),
+    "aff_knn": (I32, [P, I64, I64, P, I64, I64, I32, I32, I32, I32, I32, P, I32, P, P, SZ, P]),
+    "aff_nbhd_attn_fwd": (I32, [ctypes.POINTER(NbhdAttnArgs), P]),
+}
+
+_lib = None
+
+
+class AffLaunchError(RuntimeError):
+    """The HIP runtime rejected a kernel launch."""
+
+
+def load() -> ctypes.CDLL:
+    """Load libaffmae.so and declare its signatures (raises if it is not built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is not built; run `python -m affmae_amd.build_lib` "
+                "(there is no CPU fallback for the HIP kernels)")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        ver = lib.aff_abi_version()
+        if ver != ABI_VERSION:
+            raise RuntimeError(f"libaffmae ABI version {ver} != expected {ABI_VERSION}; rebuild")
+        _lib = lib
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status == AFF_OK:
+        return
+    msg = load().aff_last_error().decode(errors="replace")
+    if status == AFF_ERR_INVALID_ARG:
+        raise ValueError(f"{what}: {msg}")
+    if status == AFF_ERR_UNSUPPORTED:
+        raise NotImplementedError(f"{what}: {msg}")
+    if status == AFF_ERR_WORKSPACE:
+        raise RuntimeError(f"{what}: {msg}")
+    raise AffLaunchError(f"{what}: {msg}")
+
+
+def stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_cuda(*tensors: torch.Tensor) -> torch.device:
+    """Assert that every tensor lives on one GPU (the reference asserts the same)."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        assert t.is_cuda, "Inputs must be on CUDA"
+        if dev is None:
+            dev = t.device
+        assert t.device == dev, f"all inputs must be on one device ({dev} vs {t.device})"
+    return dev

@@ -1,0 +1,24 @@
+// Library-wide C entry points: error reporting and ABI version.
+#include "common.hpp"
+
+#include <string.h>
+
+namespace aff {
+
+static thread_local char g_last_error[512] = "";
+
+aff_status fail(aff_status code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+void clear_error() { g_last_error[0] = '\0'; }
+
+}  // namespace aff
+
+extern "C" const char *aff_last_error(void) { return aff::g_last_error; }
+
+extern "C" int aff_abi_version(void) { return 2; }

@@ -1,0 +1,222 @@
+"""Neighbourhood (cluster) flash attention on gfx950.
+
+Drop-in for src/layers/kernels/local_attn.py of the reference:
+``launch_flash_nbhood_attn_fwd`` (local_attn.py:609-708) and
+``FlashLocalAttentionFunction`` (local_attn.py:843-936) keep their names,
+arguments, assertion messages and output shapes.  Differences by design:
+inputs are not cast to fp16 (fp32, fp16 and bf16 run natively) and the
+output keeps the input dtype without an fp16 round trip (local_attn.py:340).
+
+``nbhd_attn_fwd`` is the extended entry used by ClusterAttention: strided
+q/k/v/out views (no permute copies) and the bias either dense, gathered from
+a [T*T, H] table by pe_idx, or computed from coordinates in-kernel.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+from torch.autograd import Function
+from torch.amp import custom_fwd, custom_bwd
+
+from .. import _lib
+from ..utils.pos_embed import REL_POS_WIDTH
+
+_SUPPORTED_D = (8, 16, 32, 64, 128)
+
+
+def _row_ok(t: torch.Tensor) -> bool:
+    """Unit stride on the last dim and 16-byte aligned rows."""
+    if t.stride(-1) != 1:
+        return False
+    es = t.element_size()
+    if t.data_ptr() % 16:
+        return False
+    return all((s * es) % 16 == 0 for s in t.stride()[:-1])
+
+
+def _prep_qkv(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    if t.dtype != dtype:
+        t = t.to(dtype)
+    if not _row_ok(t):
+        t = t.contiguous()
+    return t
+
+
+def _idx(t: torch.Tensor) -> torch.Tensor:
+    if t.dtype not in (torch.int32, torch.int64):
+        t = t.to(torch.int64)
+    if t.stride(-1) != 1:
+        t = t.contiguous()
+    return t
+
+
+def nbhd_attn_fwd(q, k, v, member_idx, scale, *, bias=None, pe_idx=None, pe_table=None,
+                  pos=None, pos_weight=None, pos_bias=None, rel_width=REL_POS_WIDTH, mask=None,
+                  blank_k=None, blank_v=None, out=None, return_lse=True):
+    """Neighbourhood attention forward through aff_nbhd_attn_fwd.
+
+    q, k, v   : [B,H,N,D] (any strides with a unit stride on D), one dtype
+    member_idx: [B,N,M] int32/int64
+    bias      : dense [B,H,N,M], or
+    pe_idx + pe_table: bias[b,h,n,j] = pe_table[pe_idx[b,n,j], h], or
+    pos + pe_table: as above with pe_idx computed in-kernel from the
+                coordinates exactly as the encoder does (aff.py:458-465), or
+    pos + pos_weight [H,5] + pos_bias [H]: continuous relative-position bias
+    mask      : [B,1|H,N,M] (nonzero = valid) or None
+    blank_k/v : [H,D] or None
+    out       : optional [B,H,N,D] view to write into (e.g. a [B,N,H,D] buffer
+                permuted), otherwise allocated contiguous [B,H,N,D]
+    Returns (out, lse [B,H,N] fp32 or None).
+    """
+    lib = _lib.load()
+    dev = _lib.require_cuda(q, k, v, member_idx, bias, pe_idx, pe_table, pos, mask, blank_k, blank_v)
+    dtype = q.dtype
+    if dtype not in _lib.DTYPE_CODE:
+        raise NotImplementedError(f"dtype {dtype} not supported")
+    B, H, N, D = q.shape
+    M = member_idx.shape[-1]
+    assert k.shape == q.shape and v.shape == q.shape, "q, k, v must have the same shape"
+    assert tuple(member_idx.shape) == (B, N, M), f"member_idx must be [B,N,M], got {tuple(member_idx.shape)}"
+    if D not in _SUPPORTED_D:
+        raise NotImplementedError(f"head_dim {D} not compiled (supported: {_SUPPORTED_D})")
+    q = _prep_qkv(q, dtype)
+    k = _prep_qkv(k, dtype)
+    v = _prep_qkv(v, dtype)
+    mi = _idx(member_idx)
+    if out is None:
+        out = torch.empty((B, H, N, D), dtype=dtype, device=dev)
+    else:
+        assert tuple(out.shape) == (B, H, N, D) and out.dtype == dtype and _row_ok(out), "bad out view"
+    lse = torch.empty((B, H, N), dtype=torch.float32, device=dev) if return_lse else None
+
+    a = _lib.NbhdAttnArgs()
+    a.dtype = _lib.DTYPE_CODE[dtype]
+    a.B, a.H, a.N, a.M, a.D = B, H, N, M, D
+    a.scale = float(scale)
+    a.q, (a.q_sb, a.q_sh, a.q_sn) = q.data_ptr(), q.stride()[:3]
+    a.k, (a.k_sb, a.k_sh, a.k_sn) = k.data_ptr(), k.stride()[:3]
+    a.v, (a.v_sb, a.v_sh, a.v_sn) = v.data_ptr(), v.stride()[:3]
+    a.member_idx = mi.data_ptr()
+    a.idx_is_i64 = 1 if mi.dtype == torch.int64 else 0
+    a.mi_sb, a.mi_sn = mi.stride(0), mi.stride(1)
+    keep = [q, k, v, mi, out]
+
+    if bias is not None and bias.numel() > 0:
+        assert tuple(bias.shape) == (B, H, N, M), \
+            "bias must have shape [batch_size, n_heads, seq_len, neighbor_size]"
+        bt = bias if bias.dtype in _lib.DTYPE_CODE else bias.to(torch.float32)
+        if bt.stride(-1) != 1:
+            bt = bt.contiguous()
+        a.bias_mode = 1
+        a.bias, a.bias_dtype = bt.data_ptr(), _lib.DTYPE_CODE[bt.dtype]
+        a.bias_sb, a.bias_sh, a.bias_sn = bt.stride()[:3]
+        keep.append(bt)
+    elif pe_idx is not None:
+        assert pe_table is not None and pe_table.dim() == 2 and pe_table.shape[1] == H, \
+            "pe_table must be [rows, H]"
+        assert tuple(pe_idx.shape) == (B, N, M), "pe_idx must be [B,N,M]"
+        tb = pe_table if pe_table.dtype in _lib.DTYPE_CODE else pe_table.to(torch.float32)
+        tb = tb.contiguous()
+        pe = _idx(pe_idx)
+        a.bias_mode = 2
+        a.pe_idx, a.pe_is_i64 = pe.data_ptr(), 1 if pe.dtype == torch.int64 else 0
+        a.pe_sb, a.pe_sn = pe.stride(0), pe.stride(1)
+        a.table, a.table_dtype, a.table_rows = tb.data_ptr(), _lib.DTYPE_CODE[tb.dtype], tb.shape[0]
+        keep += [tb, pe]
+    elif pos is not None and pe_table is not None:
+        assert pe_table.dim() == 2 and pe_table.shape[1] == H, "pe_table must be [rows, H]"
+        assert tuple(pos.shape) == (B, N, 2), "pos must be [B,N,2]"
+        tb = pe_table if pe_table.dtype in _lib.DTYPE_CODE else pe_table.to(torch.float32)
+        tb = tb.contiguous()
+        p = pos.to(torch.float32)
+        if p.stride(-1) != 1:
+            p = p.contiguous()
+        a.bias_mode = 4
+        a.pos, a.pos_sb, a.pos_sn = p.data_ptr(), p.stride(0), p.stride(1)
+        a.rel_width = int(rel_width)
+        a.table, a.table_dtype, a.table_rows = tb.data_ptr(), _lib.DTYPE_CODE[tb.dtype], tb.shape[0]
+        keep += [p, tb]
+    elif pos is not None:
+        assert pos_weight is not None and pos_bias is not None
+        assert tuple(pos.shape) == (B, N, 2), "pos must be [B,N,2]"
+        assert tuple(pos_weight.shape) == (H, 5) and tuple(pos_bias.shape) == (H,)
+        p = pos.to(torch.float32)
+        if p.stride(-1) != 1:
+            p = p.contiguous()
+        w = pos_weight.detach().to(torch.float32).contiguous()
+        bb = pos_bias.detach().to(torch.float32).contiguous()
+        a.bias_mode = 3
+        a.pos, a.pos_sb, a.pos_sn = p.data_ptr(), p.stride(0), p.stride(1)
+        a.pos_w, a.pos_b = w.data_ptr(), bb.data_ptr()
+        keep += [p, w, bb]
+    else:
+        a.bias_mode = 0
+
+    if mask is not None and mask.numel() > 0:
+        if mask.dim() == 3:
+            mask = mask.unsqueeze(1)
+        assert mask.shape[0] == B and mask.shape[1] in (1, H) and tuple(mask.shape[2:]) == (N, M), \
+            f"mask must have shape [batch_size, n_heads, seq_len, neighbor_size] (mask shape: {tuple(mask.shape)})"
+        mk = (mask > 0) if mask.dtype != torch.bool else mask
+        mk = mk.to(torch.uint8)
+        if mk.stride(-1) != 1:
+            mk = mk.contiguous()
+        a.mask = mk.data_ptr()
+        a.mask_sb, a.mask_sh, a.mask_sn = mk.stride(0), (mk.stride(1) if mk.shape[1] == H and H > 1 else 0), mk.stride(2)
+        keep.append(mk)
+
+    if blank_k is not None and blank_v is not None and blank_k.numel() > 0 and blank_v.numel() > 0:
+        assert tuple(blank_k.shape) == (H, D), "blank_k must have shape [n_heads, head_dim]"
+        assert tuple(blank_v.shape) == (H, D), "blank_v must have shape [n_heads, head_dim]"
+        bk = blank_k.detach().to(dtype).contiguous()
+        bv = blank_v.detach().to(dtype).contiguous()
+        a.blank_k, a.blank_v = bk.data_ptr(), bv.data_ptr()
+        keep += [bk, bv]
+
+    a.out, (a.o_sb, a.o_sh, a.o_sn) = out.data_ptr(), out.stride()[:3]
+    a.lse = lse.data_ptr() if lse is not None else None
+    st = lib.aff_nbhd_attn_fwd(ctypes.byref(a), _lib.stream_ptr(dev))
+    _lib.check(st, "aff_nbhd_attn_fwd")
+    del keep
+    return out, lse
+
+
+def launch_flash_nbhood_attn_fwd(q, k, v, member_index, sm_scale, bias=None, mask=None,
+                                 blank_k=None, blank_v=None, exp2=False):
+    """(o [B,H,N,D] in q.dtype, lse [B,H,N] fp32) — reference local_attn.py:609-708.
+
+    ``exp2`` is accepted for compatibility; the result is the same function.
+    """
+    assert q.shape == k.shape and k.shape == v.shape, "q, k, v must have the same shape"
+    assert q.dim() == 4 and q.shape == k.shape and q.shape == v.shape, "q, k, v must have 4 dimensions"
+    assert q.shape[-1] == k.shape[-1] and k.shape[-1] == v.shape[-1], "q, k, v must have the same head dimension"
+    assert q.shape[-1] % 8 == 0, "head_dim must be a multiple of 8"
+    batch_size, n_heads, seq_len, head_dim = q.shape
+    neighbor_size = member_index.shape[-1]
+    assert neighbor_size % 8 == 0, "neighbor_size must be a multiple of 8"
+    if mask is not None and mask.numel() > 0 and mask.shape[1] == 1:
+        mask = mask.expand(batch_size, 1, seq_len, neighbor_size)
+    return nbhd_attn_fwd(q, k, v, member_index, sm_scale, bias=bias, mask=mask,
+                         blank_k=blank_k, blank_v=blank_v, return_lse=True)
+
+
+class FlashLocalAttentionFunction(Function):
+    """Autograd entry point (reference local_attn.py:843-936).
+
+    forward(Q, K, V, member_idx, bias, mask, blank_k, blank_v, softmax_scale)
+    -> [B,H,N,D] in Q's dtype.  The backward kernels are not built yet and
+    raise NotImplementedError.
+    """
+
+    @staticmethod
+    @custom_fwd(device_type="cuda")
+    def forward(ctx, Q, K, V, member_idx, bias, mask, blank_k, blank_v, softmax_scale):
+        out, _ = launch_flash_nbhood_attn_fwd(Q, K, V, member_idx, softmax_scale, bias=bias, mask=mask,
+                                              blank_k=blank_k, blank_v=blank_v)
+        return out
+
+    @staticmethod
+    @custom_bwd(device_type="cuda")
+    def backward(ctx, grad_output):
+        raise NotImplementedError("neighbourhood attention backward is not implemented in affmae_amd yet")
