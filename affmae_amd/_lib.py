@@ -55,6 +55,26 @@ class NbhdAttnArgs(ctypes.Structure):
     ]
 
 
+DEFORM_MAX_LEVELS = 8
+DEFORM_SHEPARD, DEFORM_IDW = 0, 1
+
+
+class DeformArgs(ctypes.Structure):
+    """Mirror of ``aff_deform_args`` (include/affmae.h)."""
+    _fields_ = [
+        ("mode", I32), ("B", I32), ("Nq", I32), ("H", I32), ("L", I32), ("P", I32), ("K", I32), ("C", I32),
+        ("query_pos", P), ("qp_sb", I64), ("qp_sn", I64),
+        ("kv_pos", P), ("kp_sb", I64), ("kp_sn", I64),
+        ("level_start", I32 * (DEFORM_MAX_LEVELS + 1)),
+        ("offsets", P), ("off_dtype", I32), ("off_sb", I64), ("off_sn", I64), ("off_sh", I64),
+        ("attn", P), ("attn_dtype", I32), ("at_sb", I64), ("at_sn", I64), ("at_sh", I64),
+        ("dtype", I32), ("values", P), ("v_sb", I64), ("v_sn", I64), ("v_sh", I64),
+        ("power", P),
+        ("out", P), ("o_sb", I64), ("o_sn", I64), ("o_sh", I64),
+        ("knn_idx", P), ("knn_d2", P),
+    ]
+
+
 # Every symbol include/affmae.h declares, with (restype, argtypes).
 SIGNATURES = {
     "aff_last_error": (ctypes.c_char_p, []),
@@ -62,6 +82,18 @@ SIGNATURES = {
     "aff_knn_workspace_bytes": (SZ, [I32, I32, I32, I32, I32]),
     "aff_knn": (I32, [P, I64, I64, P, I64, I64, I32, I32, I32, I32, I32, P, I32, P, P, SZ, P]),
     "aff_nbhd_attn_fwd": (I32, [ctypes.POINTER(NbhdAttnArgs), P]),
+    "aff_weighted_features_fwd": (I32, [P, I32, I64, I64, I64, I64, P, I32, I64, I64, P, I32, I64, I64,
+                                        I32, I32, I32, I32, I32, I32, P, I64, I64, I64, P]),
+    "aff_weighted_gather_fwd": (I32, [P, I32, I64, I64, P, I32, I64, I64, P, I32, I64, I64,
+                                      I32, I32, I32, I32, I32, P, I64, I64, P]),
+    "aff_softmax_merge_fwd": (I32, [P, I64, I64, P, I64, I64, P, I32, I64, I64, P, I32, I64, I64,
+                                    I32, I32, I32, I32, I32, F32, P, I64, I64, P, I64, I64, P, P]),
+    "aff_deform_workspace_bytes": (SZ, [ctypes.POINTER(DeformArgs)]),
+    "aff_deform_fwd": (I32, [ctypes.POINTER(DeformArgs), P, SZ, P]),
+    "aff_deform_sample_fwd": (I32, [I32, P, I64, I64, P, I64, I64, P, I32, I64, I64, P, I32, I32, I32, I32, I32,
+                                    P, I32, I64, I64, P, I32, I64, I64, I32, P, I64, I64, P, I32, I64, I64, P]),
+    "aff_msdetrpc_fwd": (I32, [P, I32, I64, I64, I64, P, I32, I64, I64, I64, P, I32, I64, I64, P, I32, I64, I64,
+                               I32, I32, I32, I32, I32, I32, P, I64, I64, P]),
 }
 
 _lib = None

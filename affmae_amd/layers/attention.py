@@ -1,5 +1,10 @@
 """Attention modules with the reference's signatures (src/layers/attention.py).
 
+``DeformableCrossAttention`` / ``DeformableSelfAttention`` (attention.py:210-593)
+keep the reference's constructors, forwards, parameter names and
+initialisation; their fused branch runs the in-kernel K-NN deformable
+kernel, the other branches the given-index and MSDETRPC kernels.
+
 ``ClusterAttention`` keeps the constructor, forward signature, parameter and
 buffer names of the reference (attention.py:20-207) so state_dicts load
 unchanged.  Its local branch runs the HIP neighbourhood-attention kernel
@@ -11,11 +16,20 @@ order so the projection reads it without a permute.
 """
 from __future__ import annotations
 
+import math
+
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from ..kernels.fused_deform_attn import (
+    fused_deformable_attention,
+    fused_knn_deformable_cross_attention,
+    fused_knn_deformable_self_attention,
+)
+from ..kernels.knn import knn as hip_knn
 from ..kernels.local_attn import nbhd_attn_fwd
+from ..kernels.msdetrpc import MSDETRPCFunction
 from ..utils.pos_embed import pre_table_fp16, pre_table_fp32
 
 
@@ -118,3 +132,120 @@ class ClusterAttention(nn.Module):
         out = F.scaled_dot_product_attention(qh, k_full, v_full, attn_mask=bias)
         out = out.permute(0, 2, 1, 3).reshape(B, N, C)
         return self.proj_drop(self.proj(out))
+
+
+# ------------------------------------------------------------------ deformable --
+def _deform_reset(mod):
+    """Parameter initialisation of the reference (attention.py:247-273)."""
+    nn.init.constant_(mod.sampling_offsets.weight.data, 0.)
+    thetas = torch.arange(mod.n_heads, dtype=torch.float32) * (2.0 * math.pi / mod.n_heads)
+    grid_init = torch.stack([thetas.cos(), thetas.sin()], -1)
+    grid_init = (grid_init / grid_init.abs().max(-1, keepdim=True)[0]).view(mod.n_heads, 1, 2).repeat(1, mod.n_points, 1)
+    for i in range(mod.n_points):
+        grid_init[:, i, :] *= i + 1
+    with torch.no_grad():
+        mod.sampling_offsets.bias = nn.Parameter(grid_init.view(-1))
+    nn.init.constant_(mod.attention_weights.weight.data, 0.)
+    nn.init.constant_(mod.attention_weights.bias.data, 0.)
+    nn.init.xavier_uniform_(mod.value_proj.weight.data)
+    nn.init.constant_(mod.value_proj.bias.data, 0.)
+    nn.init.xavier_uniform_(mod.output_proj.weight.data)
+    nn.init.constant_(mod.output_proj.bias.data, 0.)
+
+
+def _deform_unfused(mod, query_pos, kv_pos, sampling_offsets, attention_weights, key_value_proj):
+    """The reference's non-fused branches (attention.py:319-399): knn(k=4) of
+    every sampling location, then the given-index fused kernel (use_fused) or
+    explicit Shepard weights + MSDETRPC."""
+    b, n_q, h, k, _ = sampling_offsets.shape
+    n_kv = kv_pos.shape[1]
+    c_ = mod.c_
+    values = key_value_proj.reshape(b, n_kv, h, c_).permute(0, 2, 1, 3).reshape(b * h, n_kv, c_)
+    loc = query_pos.unsqueeze(2).unsqueeze(3) + sampling_offsets
+    loc = loc.permute(0, 2, 1, 3, 4).reshape(b * h, n_q * k, 2).contiguous()
+    kv_loc = kv_pos.unsqueeze(1).expand(-1, h, -1, -1).reshape(b * h, n_kv, 2).contiguous()
+    nb_idx = hip_knn(loc, kv_loc, k=4)
+    if mod.use_fused:
+        aw = attention_weights.permute(0, 2, 1, 3).reshape(b * h, n_q * k)
+        out = fused_deformable_attention(loc, kv_loc, nb_idx, mod.shepard_power, aw, values, D=2)
+        out = out.reshape(b * h, n_q, k, c_).sum(dim=2)
+        return out.reshape(b, h, n_q, c_).permute(0, 2, 1, 3).reshape(b, n_q, h * c_)
+    nb_pos = torch.gather(kv_loc.unsqueeze(1).expand(-1, n_q * k, -1, -1), 2,
+                          nb_idx.unsqueeze(-1).expand(-1, -1, -1, 2))
+    dist = torch.norm(nb_pos - loc.unsqueeze(2), dim=-1, p=2) + 1e-6
+    power = F.relu(mod.shepard_power) + 1e-6
+    nn_weights = F.softmax(-power * dist.unsqueeze(-1), dim=-2)
+    out = MSDETRPCFunction.apply(nb_idx.reshape(b * h, n_q, k, 4), nn_weights.reshape(b * h, n_q, k, 4),
+                                 attention_weights.permute(0, 2, 1, 3).reshape(b * h, n_q, k), values)
+    return out.reshape(b, h, n_q, c_).permute(0, 2, 1, 3).reshape(b, n_q, h * c_)
+
+
+class DeformableCrossAttention(nn.Module):
+    """Single-level deformable cross attention (reference attention.py:210-404)."""
+
+    def __init__(self, d_model, n_heads, n_points, shepard_power=3.0, shepard_power_learnable=True,
+                 use_fused=False, use_fused_knn=True):
+        super().__init__()
+        self.d_model = d_model
+        self.n_heads = n_heads
+        self.n_points = n_points
+        self.c_ = d_model // n_heads
+        self.use_fused = use_fused
+        self.use_fused_knn = use_fused_knn
+        self.sampling_offsets = nn.Linear(d_model, n_heads * n_points * 2)
+        self.attention_weights = nn.Linear(d_model, n_heads * n_points)
+        self.value_proj = nn.Linear(d_model, d_model)
+        self.output_proj = nn.Linear(d_model, d_model)
+        self.shepard_power = nn.Parameter(torch.tensor(1.0))
+        _deform_reset(self)
+
+    def forward(self, query, query_pos, key_value, kv_pos):
+        """query [b,n_q,c], query_pos [b,n_q,2], key_value [b,n_kv,c], kv_pos [b,n_kv,2] -> [b,n_q,c]."""
+        b, n_q, c = query.shape
+        n_kv = key_value.shape[1]
+        h, k, c_ = self.n_heads, self.n_points, self.c_
+        offs = self.sampling_offsets(query).view(b, n_q, h, k, 2)
+        attn = F.softmax(self.attention_weights(query).view(b, n_q, h, k), dim=-1)
+        vproj = self.value_proj(key_value)
+        if self.use_fused_knn and k == 4:
+            out = fused_knn_deformable_cross_attention(query_pos, kv_pos, offs, attn,
+                                                       vproj.view(b, n_kv, h, c_), self.shepard_power, D=2)
+            out = out.reshape(b, n_q, c)
+        else:
+            out = _deform_unfused(self, query_pos, kv_pos, offs, attn, vproj)
+        return self.output_proj(out)
+
+
+class DeformableSelfAttention(nn.Module):
+    """Single-level deformable self attention (reference attention.py:407-593)."""
+
+    def __init__(self, d_model, n_heads, n_points, shepard_power=3.0, shepard_power_learnable=True,
+                 use_fused=False, use_fused_knn=True):
+        super().__init__()
+        self.d_model = d_model
+        self.n_heads = n_heads
+        self.n_points = n_points
+        self.c_ = d_model // n_heads
+        self.use_fused = use_fused
+        self.use_fused_knn = use_fused_knn
+        self.sampling_offsets = nn.Linear(d_model, n_heads * n_points * 2)
+        self.attention_weights = nn.Linear(d_model, n_heads * n_points)
+        self.value_proj = nn.Linear(d_model, d_model)
+        self.output_proj = nn.Linear(d_model, d_model)
+        self.shepard_power = nn.Parameter(torch.tensor(1.0))
+        _deform_reset(self)
+
+    def forward(self, x, pos):
+        """x [b,n,c], pos [b,n,2] -> [b,n,c]."""
+        b, n, c = x.shape
+        h, k, c_ = self.n_heads, self.n_points, self.c_
+        offs = self.sampling_offsets(x).view(b, n, h, k, 2)
+        attn = F.softmax(self.attention_weights(x).view(b, n, h, k), dim=-1)
+        vproj = self.value_proj(x)
+        if self.use_fused_knn and k == 4:
+            out = fused_knn_deformable_self_attention(pos, offs, attn, vproj.view(b, n, h, c_),
+                                                      self.shepard_power, D=2)
+            out = out.reshape(b, n, c)
+        else:
+            out = _deform_unfused(self, pos, pos, offs, attn, vproj)
+        return self.output_proj(out)

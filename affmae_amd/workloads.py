@@ -63,3 +63,64 @@ def cfg2(B: int = 32, N: int = 6272, H: int = 4, D: int = 32, dtype=torch.bfloat
     blank_k = (torch.randn((H, D), generator=g2) * 0.2).to(dtype)
     blank_v = (torch.randn((H, D), generator=g2) * 0.2).to(dtype)
     return dict(pos=pos, q=q, k=k, v=v, pos_w=pos_w, pos_b=pos_b, blank_k=blank_k, blank_v=blank_v)
+
+
+def cfg3(B: int = 32, N: int = 6272, M: int = 2509, C: int = 128, dtype=torch.bfloat16):
+    """Config 3: weighted-gather downsampling merge at ratio 0.4.
+
+    Source tokens: config-2 coordinates normalised by the grid side (112) and
+    features ~ N(0, 1) [B, N, C].  Merged points: M tokens per image drawn
+    without replacement with probability proportional to an importance score
+    U(0, 1) (seed 3), listed in source order; their coordinates are the
+    selected tokens' coordinates.  Returns CPU tensors src_pos, feat, sel
+    [B, M] int64, merged_pos.
+    """
+    src_pos = jittered_grid(B, 112, N, seed=0) / 112.0
+    feat = torch.randn((B, N, C), generator=_gen(1)).to(dtype)
+    g = _gen(3)
+    sel = torch.empty((B, M), dtype=torch.int64)
+    for b in range(B):
+        imp = torch.rand(N, generator=g)
+        sel[b] = torch.multinomial(imp, M, replacement=False, generator=g).sort().values
+    merged_pos = src_pos.gather(1, sel.unsqueeze(-1).expand(-1, -1, 2))
+    return dict(src_pos=src_pos, feat=feat, sel=sel, merged_pos=merged_pos)
+
+
+def cfg4(B: int = 32, H: int = 8, C: int = 32, P: int = 4, level_sizes=(6272, 2509, 1004, 402),
+         dtype=torch.bfloat16, side: int = 112):
+    """Config 4: multi-level deformable cross-attention of a dense pixel decoder.
+
+    Queries: the side x side grid cell centres ((i + 0.5) / side), identical for
+    every image.  Level 0: config-2 coordinates normalised by the side; level
+    l + 1: a seeded subset of level l (probability proportional to U(0, 1)
+    importance, without replacement).  Values [B, sum N_l, H, C] ~ N(0, 1);
+    offsets [B, Nq, H, L, P, 2] ~ N(0, 0.02); attention logits ~ N(0, 1)
+    softmaxed over L * P.  Returns CPU tensors and level_start.
+    """
+    L = len(level_sizes)
+    lv0 = jittered_grid(B, side, level_sizes[0], seed=0) / float(side)
+    levels = [lv0]
+    g = _gen(3)
+    for l in range(1, L):
+        prev = levels[-1]
+        sub = torch.empty((B, level_sizes[l], 2), dtype=torch.float32)
+        for b in range(B):
+            imp = torch.rand(prev.shape[1], generator=g)
+            sel = torch.multinomial(imp, level_sizes[l], replacement=False, generator=g).sort().values
+            sub[b] = prev[b, sel]
+        levels.append(sub)
+    kv_pos = torch.cat(levels, dim=1)
+    level_start = [0]
+    for n in level_sizes:
+        level_start.append(level_start[-1] + n)
+    ax = (torch.arange(side, dtype=torch.float32) + 0.5) / side
+    ys, xs = torch.meshgrid(ax, ax, indexing="ij")
+    qpos = torch.stack([xs, ys], -1).reshape(1, side * side, 2).expand(B, -1, -1).contiguous()
+    Nq = side * side
+    gv = _gen(1)
+    values = torch.randn((B, level_start[-1], H, C), generator=gv).to(dtype)
+    go = _gen(2)
+    offsets = (torch.randn((B, Nq, H, L, P, 2), generator=go) * 0.02).to(dtype)
+    logits = torch.randn((B, Nq, H, L * P), generator=go)
+    attn = torch.softmax(logits, dim=-1).reshape(B, Nq, H, L, P).to(dtype)
+    return dict(query_pos=qpos, kv_pos=kv_pos, level_start=level_start, values=values, offsets=offsets, attn=attn)

@@ -52,6 +52,70 @@ def knn_bytes() -> int:
     return B * N * 2 * 4 + B * N * K_NN * 4
 
 
+def cfg3_bytes(B3, N3, M3, C3, k) -> int:
+    """Softmax merge: features, coordinates and indices in; features and coordinates out."""
+    return B3 * N3 * C3 * 2 + B3 * M3 * k * 4 + B3 * N3 * 2 * 4 + B3 * M3 * 2 * 4 + B3 * M3 * C3 * 2 + B3 * M3 * 2 * 4
+
+
+def cfg4_bytes(w) -> int:
+    """Multi-level deformable attention: offsets, attention, query and level coordinates,
+    values in; output out (every tensor once)."""
+    el = lambda t: t.numel() * t.element_size()
+    B4, Nq, H4, L4, P4, _ = w["offsets"].shape
+    C4 = w["values"].shape[-1]
+    return (el(w["offsets"]) + el(w["attn"]) + el(w["query_pos"]) + el(w["kv_pos"]) + el(w["values"])
+            + B4 * Nq * H4 * C4 * w["values"].element_size())
+
+
+def time_events(fn, reps: int):
+    """Average duration (ms) of fn() over reps, HIP events on the current stream."""
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    s = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    for i in range(reps):
+        s[i].record()
+        fn()
+        e[i].record()
+    torch.cuda.synchronize()
+    return sum(s[i].elapsed_time(e[i]) for i in range(reps)) / reps
+
+
+def other_configs(dev, reps: int):
+    """Configs 3 and 4 at full size: kernel times and HBM fractions."""
+    import torch
+    from affmae_amd import workloads
+    from affmae_amd.kernels.knn import knn_launch
+    from affmae_amd.kernels.weighted_gather import softmax_merge_launch
+    from affmae_amd.kernels.fused_deform_attn import ms_deformable_attention
+
+    res = {}
+    w3 = workloads.cfg3(B=32)
+    sp, mp, f = w3["src_pos"].to(dev), w3["merged_pos"].to(dev), w3["feat"].to(dev)
+    idx = knn_launch(mp, sp, 48, out_dtype=torch.int32)
+    fo = torch.empty((32, 2509, 128), dtype=torch.bfloat16, device=dev)
+    po = torch.empty((32, 2509, 2), dtype=torch.float32, device=dev)
+    t_merge = time_events(lambda: softmax_merge_launch(mp, sp, f, idx, 0.1, out=fo, out_pos=po), reps)
+    t_knn3 = time_events(lambda: knn_launch(mp, sp, 48, out_dtype=torch.int32), reps)
+    b3 = cfg3_bytes(32, 6272, 2509, 128, 48)
+    res["cfg3_softmax_merge"] = {"ms": t_merge, "algorithmic_bytes": b3,
+                                 "hbm_frac": b3 / (t_merge * 1e-3) / HBM_PEAK,
+                                 "merged_points_per_s": 32 * 2509 / (t_merge * 1e-3),
+                                 "knn_k48_ms": t_knn3}
+    del sp, mp, f, idx, fo, po
+    w4 = workloads.cfg4(B=32)
+    g4 = {n: (v.to(dev) if torch.is_tensor(v) else v) for n, v in w4.items()}
+    t_def = time_events(lambda: ms_deformable_attention(g4["query_pos"], g4["kv_pos"], g4["level_start"],
+                                                        g4["offsets"], g4["attn"], g4["values"], power=3.0, k=3,
+                                                        weighting="idw"), reps)
+    b4 = cfg4_bytes(w4)
+    res["cfg4_ms_deform_idw"] = {"ms": t_def, "algorithmic_bytes": b4,
+                                 "hbm_frac": b4 / (t_def * 1e-3) / HBM_PEAK,
+                                 "queries_per_s": 32 * 12544 / (t_def * 1e-3)}
+    return res
+
+
 def cpu_baseline(w, table_cpu, budget_s: float):
     """Oracle KNN + fp64 oracle attention on whole images until the budget is spent."""
     import numpy as np
@@ -90,6 +154,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-oracle work (0 = skip)")
+    ap.add_argument("--no-other", action="store_true", help="skip the config-3/4 kernel timings")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -143,6 +208,12 @@ def main() -> int:
     a_bytes = attn_bytes(table.shape[0])
     achieved = a_bytes / (attn_ms * 1e-3)
 
+    other = None
+    if not args.no_other:
+        del w
+        other = other_configs(dev, reps=10)
+        w = workloads.cfg2(B=B, N=N, H=H, D=D)
+
     cpu = None
     if args.cpu_budget > 0:
         cpu = cpu_baseline(w, table.cpu(), args.cpu_budget)
@@ -180,6 +251,7 @@ def main() -> int:
             "algorithmic_bytes": a_bytes,
         },
         "cpu_baseline": cpu,
+        "other_configs": other,
     }
     print(json.dumps(line), flush=True)
     return 0

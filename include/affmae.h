@@ -128,6 +128,164 @@ typedef struct aff_nbhd_attn_args {
 
 aff_status aff_nbhd_attn_fwd(const aff_nbhd_attn_args *args, aff_stream_t stream);
 
+/* ------------------------------------------------------------------------ *
+ * Weighted neighbour features (the AFF downsampling merge).
+ *
+ * Replaces: weighted_features() / WeightedFeaturesFunction
+ *           src/layers/kernels/weighted_features.py:401-434, kernel :30-111
+ *
+ *   out[b, i, ic, c] = sum_m weights[b, i, m, ic] * feat[b, idx[b, i, m], c]
+ *
+ * weights [B, Nout, M, IC] (w_dtype, strides w_sb, w_sn, w_sm, w_sic);
+ * feat [B, Nsrc, C] (f_dtype, unit stride on C); nbhd_idx [B, Nout, M]
+ * int32/int64 with unit stride on M; out [B, Nout, IC, C] in f_dtype with
+ * unit stride on C.  fp32 accumulation.  Indices outside [0, Nsrc)
+ * contribute nothing.
+ * ------------------------------------------------------------------------ */
+aff_status aff_weighted_features_fwd(const void *weights, int w_dtype, int64_t w_sb, int64_t w_sn,
+                                     int64_t w_sm, int64_t w_sic,
+                                     const void *feat, int f_dtype, int64_t f_sb, int64_t f_sn,
+                                     const void *nbhd_idx, int idx_is_i64, int64_t i_sb, int64_t i_sn,
+                                     int B, int Nout, int Nsrc, int M, int C, int IC,
+                                     void *out, int64_t o_sb, int64_t o_sn, int64_t o_sic,
+                                     aff_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
+ * Weighted gather: the IC = 1 case of the above.
+ *
+ * Replaces: weighted_gather() / WeightedGatherFunction
+ *           src/layers/kernels/weighted_gather.py:329-364, kernel :21-102
+ *
+ *   out[b, i, c] = sum_m weights[b, i, m] * feat[b, idx[b, i, m], c]
+ * ------------------------------------------------------------------------ */
+aff_status aff_weighted_gather_fwd(const void *nbhd_idx, int idx_is_i64, int64_t i_sb, int64_t i_sn,
+                                   const void *weights, int w_dtype, int64_t w_sb, int64_t w_sn,
+                                   const void *feat, int f_dtype, int64_t f_sb, int64_t f_sn,
+                                   int B, int Nout, int Nsrc, int M, int C,
+                                   void *out, int64_t o_sb, int64_t o_sn, aff_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
+ * Softmax-distance merge: weighted_gather with weights computed in-kernel.
+ *
+ * Replaces the composition knn -> softmax(-d / tau) -> weighted_gather on
+ * features and on coordinates (reference kernels weighted_gather.py:21-102,
+ * upsample_feature_shepard geometry.py:97-167 for the gather pattern):
+ *
+ *   d_m = sqrt(fl(fl(dx*dx) + fl(dy*dy))),  (dx, dy) = qpos[b,i] - spos[b, idx_m]
+ *   w_m = softmax_m(-d_m / tau)
+ *   out[b, i, :] = sum_m w_m feat[b, idx_m, :],  out_pos[b, i, :] = sum_m w_m spos[b, idx_m, :]
+ *
+ * query_pos [B, Nout, 2], src_pos [B, Nsrc, 2] fp32 (unit coordinate stride);
+ * feat [B, Nsrc, C] (C % 8 == 0, 16-byte aligned rows); nbhd_idx [B, Nout, K]
+ * (K <= 128, unit stride on K); out [B, Nout, C] in f_dtype; out_pos
+ * [B, Nout, 2] fp32 and out_weights [B, Nout, K] fp32 contiguous may be NULL.
+ * Indices outside [0, Nsrc) get weight 0.
+ * ------------------------------------------------------------------------ */
+aff_status aff_softmax_merge_fwd(const float *query_pos, int64_t q_sb, int64_t q_sn,
+                                 const float *src_pos, int64_t s_sb, int64_t s_sn,
+                                 const void *feat, int f_dtype, int64_t f_sb, int64_t f_sn,
+                                 const void *nbhd_idx, int idx_is_i64, int64_t i_sb, int64_t i_sn,
+                                 int B, int Nout, int Nsrc, int K, int C, float tau,
+                                 void *out, int64_t o_sb, int64_t o_sn,
+                                 float *out_pos, int64_t op_sb, int64_t op_sn, float *out_weights,
+                                 aff_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
+ * Deformable attention over point clouds with in-kernel exact K-NN.
+ *
+ * Replaces: fused_knn_deformable_cross_attention / _self_attention
+ *           src/layers/kernels/fused_deform_attn.py:4063-4119, launchers
+ *           :2387-2654, kernels :842-1011 (self) and :1188-1335 (cross);
+ *           and the multi-level composition knn(k=3) + inverse_distance_weighting
+ *           (src/utils/geometry.py:40-53) + MSDETRPC (msdetrpc.py:25-109).
+ *
+ * For every (b, q, h) and sample s = (l, p), l < L levels, p < P points:
+ *   loc  = query_pos[b, q] + offsets[b, q, h, l, p, :]            (fp32)
+ *   the K points of level l nearest to loc, exact, ties to the lower index
+ *   (d2 = fl(fl(dx*dx) + fl(dy*dy)));  fewer than K points -> all of them
+ *   mode AFF_DEFORM_SHEPARD: w_j = e_j / (sum e + 1e-8),
+ *        e_j = exp(lg_j - max lg),  lg_j = -max(power, 1e-6) * (sqrt(d2_j) + 1e-6)
+ *   mode AFF_DEFORM_IDW:     w_j = u_j / (sum u + 1e-12),  u_j = 1 / (d2_j^power + 1e-10)
+ *   out[b, q, h, :] = sum_s attn[b, q, h, l, p] * sum_j w_j * values[b, start[l] + idx_j, h, :]
+ *
+ * kv_pos [B, Ntot, 2] fp32 with level l in rows [level_start[l], level_start[l+1])
+ * (level_start[0] = 0, non-decreasing, L <= AFF_DEFORM_MAX_LEVELS; self-attention
+ * passes query_pos as kv_pos with L = 1).  offsets [B, Nq, H, L, P, 2] and attn
+ * [B, Nq, H, L, P] with strides (sb, sn, sh) and the (L, P[, 2]) block contiguous,
+ * any of fp32/fp16/bf16.  values [B, Ntot, H, C] and out [B, Nq, H, C] in `dtype`
+ * with strides (sb, sn, sh), unit stride on C, C % 8 == 0, 16-byte aligned rows.
+ * power: device pointer to one fp32 (no host synchronisation).  1 <= K <= 8,
+ * L * P <= 32.  knn_idx (int32, level-local index, -1 if missing) and knn_d2
+ * ([B, Nq, H, L, P, K] contiguous) may be NULL.  ws: aff_deform_workspace_bytes().
+ * ------------------------------------------------------------------------ */
+#define AFF_DEFORM_MAX_LEVELS 8
+enum { AFF_DEFORM_SHEPARD = 0, AFF_DEFORM_IDW = 1 };
+
+typedef struct aff_deform_args {
+    int mode;
+    int B, Nq, H, L, P, K, C;
+    const float *query_pos; int64_t qp_sb, qp_sn;
+    const float *kv_pos; int64_t kp_sb, kp_sn;
+    int level_start[AFF_DEFORM_MAX_LEVELS + 1];
+    const void *offsets; int off_dtype; int64_t off_sb, off_sn, off_sh;
+    const void *attn; int attn_dtype; int64_t at_sb, at_sn, at_sh;
+    int dtype; const void *values; int64_t v_sb, v_sn, v_sh;
+    const float *power;
+    void *out; int64_t o_sb, o_sn, o_sh;
+    int32_t *knn_idx;
+    float *knn_d2;
+} aff_deform_args;
+
+size_t aff_deform_workspace_bytes(const aff_deform_args *args);
+aff_status aff_deform_fwd(const aff_deform_args *args, void *ws, size_t ws_bytes, aff_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
+ * Distance-softmax weights from given neighbour indices, optionally gathered.
+ *
+ * Replaces: fused_deformable_attention()  fused_deform_attn.py:694-718,
+ *           launcher :503-571, kernel :79-231                  (eps_mode 0)
+ *           mssample()  src/layers/kernels/mssample.py:452-478,
+ *           launcher :300-342, kernel :17-125                  (eps_mode 1)
+ *
+ *   dist_k = eps_mode == 0 ? sqrt(d2_k) + 1e-6 : sqrt(d2_k + 1e-6),
+ *            d2_k = |sampling_locs[b, n] - kv_pos[b, idx[b, n, k]]|^2 over D <= 4 dims
+ *   w_k    = e_k / (sum e + 1e-8),  e_k = exp(-max(power, 1e-6) * dist_k - max)
+ *   weights[b, n, k] = w_k                                     (if weights != NULL)
+ *   out[b, n, :] = attn[b, n] * sum_k w_k values[b, idx_k, :]   (if out != NULL;
+ *                  attn NULL means 1)
+ * Indices outside [0, Nkv) get weight 0.  K <= 64.  power is a device scalar.
+ * values / out: `dtype`, C % 8 == 0, 16-byte aligned rows, unit stride on C.
+ * ------------------------------------------------------------------------ */
+aff_status aff_deform_sample_fwd(int eps_mode, const float *sampling_locs, int64_t l_sb, int64_t l_sn,
+                                 const float *kv_pos, int64_t k_sb, int64_t k_sn,
+                                 const void *nb_idx, int idx_is_i64, int64_t i_sb, int64_t i_sn,
+                                 const float *power, int B, int N, int Nkv, int K, int D,
+                                 const void *attn, int attn_dtype, int64_t a_sb, int64_t a_sn,
+                                 const void *values, int dtype, int64_t v_sb, int64_t v_sn, int C,
+                                 void *out, int64_t o_sb, int64_t o_sn,
+                                 void *weights, int w_dtype, int64_t w_sb, int64_t w_sn,
+                                 aff_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
+ * Multi-slot deformable gather.
+ *
+ * Replaces: MSDETRPCFunction  src/layers/kernels/msdetrpc.py:372-390,
+ *           launcher :305-325, kernel :25-109
+ *
+ *   out[b, n, c] = sum_m sum_k attn[b, n, m] * nn_weight[b, n, m, k] * val[b, nn_idx[b, n, m, k], c]
+ *
+ * nn_idx / nn_weight [B, N, M, K] (strides sb, sn, sm; unit stride on K);
+ * attn [B, N, M] (unit stride on M); val [B, Nval, C] and out [B, N, C] in
+ * `dtype`, C % 8 == 0, 16-byte aligned rows.  Indices outside [0, Nval)
+ * contribute nothing.
+ * ------------------------------------------------------------------------ */
+aff_status aff_msdetrpc_fwd(const void *nn_idx, int idx_is_i64, int64_t i_sb, int64_t i_sn, int64_t i_sm,
+                            const void *nn_weight, int w_dtype, int64_t w_sb, int64_t w_sn, int64_t w_sm,
+                            const void *attn, int a_dtype, int64_t a_sb, int64_t a_sn,
+                            const void *val, int dtype, int64_t v_sb, int64_t v_sn,
+                            int B, int N, int M, int K, int Nval, int C,
+                            void *out, int64_t o_sb, int64_t o_sn, aff_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -61,6 +61,12 @@ def lib():
         L.oracle_nbhd_attn.argtypes = [P, P, P, P, P, P, P, P, ctypes.c_double,
                                        i32, i32, i32, i32, i32, P, P]
         L.oracle_nbhd_attn.restype = i32
+        L.oracle_weighted_features.argtypes = [P, P, P, i32, i32, i32, i32, i32, i32, P]
+        L.oracle_weighted_features.restype = i32
+        L.oracle_softmax_merge.argtypes = [P, P, P, P, i32, i32, i32, i32, i32, ctypes.c_double, P, P, P]
+        L.oracle_softmax_merge.restype = i32
+        L.oracle_deform_gather.argtypes = [P, P, P, i32, i32, i32, i32, i32, i32, i32, P]
+        L.oracle_deform_gather.restype = i32
         L.oracle_num_threads.restype = i32
         L.oracle_set_num_threads.argtypes = [i32]
         _lib = L
@@ -129,6 +135,176 @@ def nbhd_attn(q, k, v, member_idx, scale: float, bias=None, mask=None, blank_k=N
     lib().oracle_nbhd_attn(_ptr(q), _ptr(k), _ptr(v), _ptr(idx), _ptr(b), _ptr(mk), _ptr(bk), _ptr(bv),
                            float(scale), B, H, N, M, D, _ptr(out), _ptr(lse))
     return out, lse
+
+
+# ------------------------------------------------------ weighted gathers ----
+def weighted_features(weights, feat, nbhd_idx):
+    """fp64 out[b,i,ic,c] = sum_m w[b,i,m,ic] f[b,idx,c] (weighted_features.py:30-111)."""
+    w = _f32(weights)
+    f = _f32(feat)
+    idx = np.ascontiguousarray(np.asarray(nbhd_idx, dtype=np.int64))
+    B, Nout, M, IC = w.shape
+    N, C = f.shape[1], f.shape[2]
+    assert idx.shape == (B, Nout, M) and f.shape[0] == B
+    out = np.empty((B, Nout, IC, C), dtype=np.float64)
+    lib().oracle_weighted_features(_ptr(w), _ptr(f), _ptr(idx), B, Nout, N, M, C, IC, _ptr(out))
+    return out
+
+
+def weighted_gather(nbhd_idx, weights, feat):
+    """fp64 out[b,i,c] = sum_m w[b,i,m] f[b,idx,c] (weighted_gather.py:21-102)."""
+    return weighted_features(np.asarray(weights)[..., None], feat, nbhd_idx)[:, :, 0, :]
+
+
+def softmax_merge(query_pos, src_pos, feat, nbhd_idx, tau):
+    """fp64 softmax(-d/tau) merge of features and coordinates.
+
+    Returns (feat_out [B,Nout,C], pos_out [B,Nout,2], weights [B,Nout,K]).
+    """
+    q = _f32(query_pos)
+    s = _f32(src_pos)
+    f = _f32(feat)
+    idx = np.ascontiguousarray(np.asarray(nbhd_idx, dtype=np.int64))
+    B, Nout, K = idx.shape
+    N, C = f.shape[1], f.shape[2]
+    out = np.empty((B, Nout, C), dtype=np.float64)
+    pos = np.empty((B, Nout, 2), dtype=np.float64)
+    w = np.empty((B, Nout, K), dtype=np.float64)
+    lib().oracle_softmax_merge(_ptr(q), _ptr(s), _ptr(f), _ptr(idx), B, Nout, N, K, C, float(tau),
+                               _ptr(out), _ptr(pos), _ptr(w))
+    return out, pos, w
+
+
+# ----------------------------------------------------------- KNN (tree) ----
+def knn_tree(query, ref, k: int):
+    """Same result as :func:`knn` (exact fp32 keys, ties to the lower index)
+    for large query sets: a scipy cKDTree proposes k + 8 candidates in fp64,
+    their fp32 d2 is recomputed and ranked by (d2, index), and a query is
+    re-run with more candidates whenever a point outside its candidate set
+    could still rank within its first k.  query [M,2], ref [N,2] fp32 (one
+    segment).  Returns (idx int64 [M,k], d2 fp32 [M,k]).
+    """
+    from scipy.spatial import cKDTree
+    q = _f32(query)
+    r = _f32(ref)
+    M, N = q.shape[0], r.shape[0]
+    assert 1 <= k <= N
+    tree = cKDTree(r.astype(np.float64))
+    idx = np.empty((M, k), dtype=np.int64)
+    d2 = np.empty((M, k), dtype=np.float32)
+    todo = np.arange(M)
+    extra = 8
+    while todo.size:
+        kk = min(N, k + extra)
+        dd, ii = tree.query(q[todo].astype(np.float64), k=kk)
+        dd = np.asarray(dd, dtype=np.float64).reshape(len(todo), kk)
+        ii = np.asarray(ii, dtype=np.int64).reshape(len(todo), kk)
+        diff = q[todo][:, None, :] - r[ii]                  # fp32, no contraction in numpy
+        c2 = (diff[..., 0] * diff[..., 0] + diff[..., 1] * diff[..., 1]).astype(np.float32)
+        order = np.lexsort((ii, c2), axis=-1)
+        ci = np.take_along_axis(ii, order, -1)[:, :k]
+        cd = np.take_along_axis(c2, order, -1)[:, :k]
+        # points outside the candidate set have fp64 distance >= dd[:, -1]
+        bound = (dd[:, -1] ** 2) * (1 - 1e-5) - 1e-30
+        safe = (kk == N) | (cd[:, -1].astype(np.float64) < bound)
+        idx[todo[safe]] = ci[safe]
+        d2[todo[safe]] = cd[safe]
+        todo = todo[~safe]
+        extra *= 4
+    return idx, d2
+
+
+# ----------------------------------------------------- deformable attention --
+def deform_weights(d2, mode: str, power: float):
+    """Per-sample neighbour weights in fp64 from fp32 squared distances.
+
+    shepard: softmax(-max(p, 1e-6) * (sqrt(d2) + 1e-6)), denominator + 1e-8
+             (fused_deform_attn.py:1296-1314);
+    idw:     (1 / (d2^p + 1e-10)) / (sum + 1e-12) (geometry.py:49-52).
+    Missing neighbours (d2 = inf) get weight 0.
+    """
+    d2 = np.asarray(d2, dtype=np.float64)
+    valid = np.isfinite(d2)
+    if mode == "shepard":
+        p = max(power, 1e-6)
+        lg = np.where(valid, -p * (np.sqrt(np.where(valid, d2, 0)) + 1e-6), -np.inf)
+        mx = lg.max(axis=-1, keepdims=True)
+        e = np.where(valid, np.exp(lg - mx), 0.0)
+        return e / (e.sum(-1, keepdims=True) + 1e-8)
+    u = np.where(valid, 1.0 / (np.where(valid, d2, 1.0) ** power + 1e-10), 0.0)
+    return u / (u.sum(-1, keepdims=True) + 1e-12)
+
+
+def deform(query_pos, kv_pos, level_start, offsets, attn, values, power: float, K: int, mode: str):
+    """fp64 deformable attention with exact per-level K-NN (the semantics of
+    aff_deform_fwd): query_pos [B,Nq,2], kv_pos [B,Ntot,2], offsets
+    [B,Nq,H,L,P,2], attn [B,Nq,H,L,P], values [B,Ntot,H,C].
+    Returns (out [B,Nq,H,C] fp64, knn_idx [B,Nq,H,L,P,K] level-local, -1 if missing).
+    """
+    qp = _f32(query_pos)
+    kp = _f32(kv_pos)
+    off = _f32(offsets)
+    at = np.asarray(attn, dtype=np.float64)
+    val = _f32(values)
+    B, Nq, H, L, P, _ = off.shape
+    C = val.shape[-1]
+    Ntot = kp.shape[1]
+    loc = (qp[:, :, None, None, None, :] + off).astype(np.float32)      # fp32 add
+    rows = np.full((B, Nq, H, L, P, K), -1, dtype=np.int64)
+    local = np.full((B, Nq, H, L, P, K), -1, dtype=np.int64)
+    d2 = np.full((B, Nq, H, L, P, K), np.inf, dtype=np.float64)
+    for b in range(B):
+        for l in range(L):
+            s0, s1 = level_start[l], level_start[l + 1]
+            n = s1 - s0
+            if n == 0:
+                continue
+            ke = min(K, n)
+            pts = loc[b, :, :, l].reshape(-1, 2)
+            ii, dd = knn_tree(pts, kp[b, s0:s1], ke)
+            local[b, :, :, l, :, :ke] = ii.reshape(Nq, H, P, ke)
+            rows[b, :, :, l, :, :ke] = ii.reshape(Nq, H, P, ke) + s0
+            d2[b, :, :, l, :, :ke] = dd.reshape(Nq, H, P, ke)
+    w = deform_weights(d2, mode, power) * at[..., None]
+    out = np.empty((B, Nq, H, C), dtype=np.float64)
+    S = L * P
+    rows_c = np.ascontiguousarray(rows.reshape(B, Nq, H, S, K))
+    w_c = np.ascontiguousarray(w.reshape(B, Nq, H, S, K))
+    lib().oracle_deform_gather(_ptr(rows_c), _ptr(w_c), _ptr(val), B, Nq, H, S, K, Ntot, C, _ptr(out))
+    return out, local
+
+
+def deform_sample(sampling_locs, kv_pos, nb_idx, power: float, eps_mode: int, attn=None, values=None):
+    """fp64 distance-softmax weights from given indices (fused_deform_attn.py:79-231
+    for eps_mode 0: sqrt(d2) + 1e-6; mssample.py:17-125 for eps_mode 1:
+    sqrt(d2 + 1e-6)), optionally gathered: returns (weights [B,N,K], out [B,N,C] or None).
+    """
+    sl = np.asarray(sampling_locs, dtype=np.float64)
+    kv = np.asarray(kv_pos, dtype=np.float64)
+    idx = np.asarray(nb_idx, dtype=np.int64)
+    B, N, K = idx.shape
+    Nkv = kv.shape[1]
+    ok = (idx >= 0) & (idx < Nkv)
+    nb = np.take_along_axis(kv, np.where(ok, idx, 0).reshape(B, -1, 1).repeat(kv.shape[2], 2), 1).reshape(B, N, K, -1)
+    d2 = ((sl[:, :, None, :] - nb) ** 2).sum(-1)
+    dist = np.sqrt(d2) + 1e-6 if eps_mode == 0 else np.sqrt(d2 + 1e-6)
+    lg = np.where(ok, -max(power, 1e-6) * dist, -np.inf)
+    e = np.where(ok, np.exp(lg - lg.max(-1, keepdims=True)), 0.0)
+    w = e / (e.sum(-1, keepdims=True) + 1e-8)
+    out = None
+    if values is not None:
+        a = np.ones((B, N)) if attn is None else np.asarray(attn, dtype=np.float64)
+        out = weighted_gather(np.where(ok, idx, -1), (w * a[..., None]).astype(np.float32), values)
+    return w, out
+
+
+def msdetrpc(nn_idx, nn_weight, attn, val):
+    """fp64 out[b,n,c] = sum_m sum_k attn[b,n,m] w[b,n,m,k] val[b, idx[b,n,m,k], c]
+    (msdetrpc.py:25-109; its commented torch form at :529-530)."""
+    idx = np.asarray(nn_idx, dtype=np.int64)
+    B, N, M, K = idx.shape
+    w = (np.asarray(attn, dtype=np.float64)[..., None] * np.asarray(nn_weight, dtype=np.float64))
+    return weighted_features(w.reshape(B, N, M * K, 1).astype(np.float32), val, idx.reshape(B, N, M * K))[:, :, 0, :]
 
 
 # ------------------------------------------------ relative-position bias ----

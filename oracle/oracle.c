@@ -183,3 +183,98 @@ int oracle_nbhd_attn(const float *q, const float *k, const float *v, const int64
     }
     return 0;
 }
+
+/* --------------------------------------------------- weighted features --
+ * weighted_features.py:30-111 (kernel) and :440-457 (its PyTorch reference):
+ *   out[b,i,ic,c] = sum_m w[b,i,m,ic] * f[b, idx[b,i,m], c]
+ * weighted_gather (weighted_gather.py:21-102) is the IC = 1 case.
+ * Indices outside [0, N) contribute nothing.  fp64 accumulation.
+ * w [B,Nout,M,IC] f32; f [B,N,C] f32; idx [B,Nout,M] int64; out [B,Nout,IC,C] f64.
+ */
+int oracle_weighted_features(const float *w, const float *f, const int64_t *idx, int B, int Nout, int N,
+                             int M, int C, int IC, double *out) {
+    int64_t rows = (int64_t)B * Nout;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) {
+        int b = (int)(r / Nout);
+        double *o = out + r * IC * C;
+        for (int64_t t = 0; t < (int64_t)IC * C; ++t) o[t] = 0.0;
+        for (int m = 0; m < M; ++m) {
+            int64_t id = idx[r * M + m];
+            if (id < 0 || id >= N) continue;
+            const float *fr = f + ((int64_t)b * N + id) * C;
+            for (int ic = 0; ic < IC; ++ic) {
+                double wv = (double)w[(r * M + m) * IC + ic];
+                for (int c = 0; c < C; ++c) o[ic * C + c] += wv * (double)fr[c];
+            }
+        }
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------ softmax merge --
+ * knn -> w = softmax_m(-d_m / tau), d_m = |q_i - s_idx_m| -> weighted_gather
+ * of features and coordinates (weighted_gather.py:21-102 applied twice).
+ * qpos [B,Nout,2], spos [B,N,2], f [B,N,C] f32; idx [B,Nout,K] int64;
+ * out [B,Nout,C], out_pos [B,Nout,2], out_w [B,Nout,K] f64.
+ * Indices outside [0, N) get weight 0.
+ */
+int oracle_softmax_merge(const float *qpos, const float *spos, const float *f, const int64_t *idx,
+                         int B, int Nout, int N, int K, int C, double tau, double *out, double *out_pos,
+                         double *out_w) {
+    int64_t rows = (int64_t)B * Nout;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) {
+        int b = (int)(r / Nout);
+        double qx = qpos[r * 2], qy = qpos[r * 2 + 1];
+        double *w = out_w + r * K;
+        double mx = -INFINITY;
+        for (int m = 0; m < K; ++m) {
+            int64_t id = idx[r * K + m];
+            if (id < 0 || id >= N) { w[m] = -INFINITY; continue; }
+            double dx = qx - spos[((int64_t)b * N + id) * 2], dy = qy - spos[((int64_t)b * N + id) * 2 + 1];
+            w[m] = -sqrt(dx * dx + dy * dy) / tau;
+            if (w[m] > mx) mx = w[m];
+        }
+        double s = 0.0;
+        for (int m = 0; m < K; ++m) { w[m] = exp(w[m] - mx); s += w[m]; }
+        double *o = out + r * C;
+        for (int c = 0; c < C; ++c) o[c] = 0.0;
+        out_pos[r * 2] = out_pos[r * 2 + 1] = 0.0;
+        for (int m = 0; m < K; ++m) {
+            w[m] /= s;
+            int64_t id = idx[r * K + m];
+            if (id < 0 || id >= N) continue;
+            const float *fr = f + ((int64_t)b * N + id) * C;
+            for (int c = 0; c < C; ++c) o[c] += w[m] * (double)fr[c];
+            out_pos[r * 2] += w[m] * (double)spos[((int64_t)b * N + id) * 2];
+            out_pos[r * 2 + 1] += w[m] * (double)spos[((int64_t)b * N + id) * 2 + 1];
+        }
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------ deformable gather --
+ * out[b,q,h,:] = sum_{s,j} w[b,q,h,s,j] * values[b, row[b,q,h,s,j], h, :]
+ * (the value gather of fused_deform_attn.py:1188-1335 / msdetrpc.py:25-109),
+ * rows < 0 skipped.  row, w [B,Nq,H,S,K]; values [B,Ntot,H,C] f32; out f64.
+ */
+int oracle_deform_gather(const int64_t *row, const double *w, const float *values, int B, int Nq, int H, int S,
+                         int K, int Ntot, int C, double *out) {
+    int64_t rows = (int64_t)B * Nq * H;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) {
+        int h = (int)(r % H);
+        int b = (int)(r / ((int64_t)Nq * H));
+        double *o = out + r * C;
+        for (int c = 0; c < C; ++c) o[c] = 0.0;
+        for (int t = 0; t < S * K; ++t) {
+            int64_t id = row[r * S * K + t];
+            if (id < 0 || id >= Ntot) continue;
+            const float *v = values + (((int64_t)b * Ntot + id) * H + h) * C;
+            double wv = w[r * S * K + t];
+            for (int c = 0; c < C; ++c) o[c] += wv * (double)v[c];
+        }
+    }
+    return 0;
+}

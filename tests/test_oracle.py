@@ -248,3 +248,154 @@ def test_golden_attention(oracle_mod, golden_dir):
                                     blank_k=g["blank_k"], blank_v=g["blank_v"])
     np.testing.assert_allclose(out, g["out"], rtol=1e-6, atol=1e-6)
     np.testing.assert_allclose(lse, g["lse"], rtol=1e-6, atol=1e-6)
+
+
+# ------------------------------------------------------ weighted gathers ----
+def test_weighted_features_matches_reference_formula(oracle_mod):
+    """Against the gather + broadcast-multiply + sum form of the reference's own
+    PyTorch check (weighted_features.py:440-457), evaluated with numpy."""
+    rng = np.random.default_rng(40)
+    B, N, Nout, M, C, IC = 2, 50, 20, 7, 12, 4
+    w = rng.standard_normal((B, Nout, M, IC)).astype(np.float32)
+    f = rng.standard_normal((B, N, C)).astype(np.float32)
+    idx = rng.integers(0, N, (B, Nout, M))
+    g = np.take_along_axis(f, idx.reshape(B, -1, 1).repeat(C, axis=2), axis=1).reshape(B, Nout, M, C)
+    ref = (w.astype(np.float64)[..., None] * g.astype(np.float64)[:, :, :, None, :]).sum(axis=2)
+    np.testing.assert_allclose(oracle_mod.weighted_features(w, f, idx), ref, rtol=1e-12, atol=1e-12)
+
+
+def test_weighted_gather_closed_forms(oracle_mod):
+    rng = np.random.default_rng(41)
+    B, N, Nout, M, C = 1, 30, 10, 5, 6
+    f = rng.standard_normal((B, N, C)).astype(np.float32)
+    idx = rng.integers(0, N, (B, Nout, M))
+    # one-hot weights pick the selected row
+    w = np.zeros((B, Nout, M), dtype=np.float32)
+    w[..., 2] = 1
+    np.testing.assert_array_equal(oracle_mod.weighted_gather(idx, w, f), f[0][idx[0, :, 2]][None])
+    # linear in the weights
+    w1 = rng.standard_normal((B, Nout, M)).astype(np.float32)
+    w2 = rng.standard_normal((B, Nout, M)).astype(np.float32)
+    lhs = oracle_mod.weighted_gather(idx, w1, f) + oracle_mod.weighted_gather(idx, w2, f)
+    np.testing.assert_allclose(lhs, oracle_mod.weighted_gather(idx, (w1 + w2).astype(np.float32), f),
+                               rtol=1e-6, atol=1e-6)
+    # out-of-range indices contribute nothing
+    bad = idx.copy()
+    bad[..., 0] = N
+    w0 = w1.copy()
+    w0[..., 0] = 0
+    np.testing.assert_allclose(oracle_mod.weighted_gather(bad, w1, f), oracle_mod.weighted_gather(idx, w0, f),
+                               rtol=1e-12)
+
+
+def test_softmax_merge_composition(oracle_mod):
+    """softmax merge == scipy softmax of -distance/tau fed to weighted_gather."""
+    rng = np.random.default_rng(42)
+    B, N, Nout, K, C = 2, 300, 40, 16, 8
+    sp = rng.random((B, N, 2), dtype=np.float32)
+    qp = rng.random((B, Nout, 2), dtype=np.float32)
+    f = rng.standard_normal((B, N, C)).astype(np.float32)
+    idx, d2 = oracle_mod.knn(qp, sp, K)
+    out, pos, w = oracle_mod.softmax_merge(qp, sp, f, idx, 0.1)
+    ww = softmax(-np.sqrt(d2.astype(np.float64)) / 0.1, axis=-1)
+    np.testing.assert_allclose(w, ww, rtol=1e-6, atol=1e-9)
+    np.testing.assert_allclose(out, oracle_mod.weighted_gather(idx, ww, f), rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(pos, oracle_mod.weighted_gather(idx, ww, sp), rtol=1e-5, atol=1e-6)
+    # very large tau -> plain mean of the neighbours
+    out, pos, w = oracle_mod.softmax_merge(qp, sp, f, idx, 1e9)
+    np.testing.assert_allclose(w, 1.0 / K, rtol=1e-7)
+    gathered = np.take_along_axis(f, idx.reshape(B, -1, 1).repeat(C, axis=2), axis=1).reshape(B, Nout, K, C)
+    np.testing.assert_allclose(out, gathered.astype(np.float64).mean(axis=2), rtol=1e-6, atol=1e-7)
+
+
+# ------------------------------------------------------------ deformable ----
+def test_knn_tree_matches_bruteforce(oracle_mod):
+    rng = np.random.default_rng(50)
+    for ref, q in [
+        (rng.random((900, 2), dtype=np.float32), rng.random((300, 2), dtype=np.float32)),
+        (rng.integers(0, 20, (900, 2)).astype(np.float32), (rng.integers(0, 40, (300, 2)) / 2).astype(np.float32)),
+    ]:
+        for k in (1, 3, 4, 8):
+            a, da = oracle_mod.knn_tree(q, ref, k)
+            b, db = oracle_mod.knn(q[None], ref[None], k)
+            np.testing.assert_array_equal(a, b[0])
+            np.testing.assert_array_equal(da, db[0])
+
+
+def test_deform_weights_closed_forms(oracle_mod):
+    # two neighbours at squared distances 1 and 4: IDW (p = 3) -> 64 : 1
+    w = oracle_mod.deform_weights(np.array([[1.0, 4.0]]), "idw", 3.0)
+    np.testing.assert_allclose(w[0], np.array([64, 1]) / 65 * (1 - 1e-12 * 65 / 64 / (1 + 1e-10)), rtol=1e-9)
+    # Shepard: equal distances -> equal weights; missing (inf) -> 0
+    w = oracle_mod.deform_weights(np.array([[0.25, 0.25, np.inf]]), "shepard", 2.0)
+    np.testing.assert_allclose(w[0], [0.5, 0.5, 0.0], rtol=1e-7)
+    # Shepard ratio exp(-p (d1 - d0))
+    w = oracle_mod.deform_weights(np.array([[1.0, 4.0]]), "shepard", 0.7)
+    np.testing.assert_allclose(w[0, 1] / w[0, 0], np.exp(-0.7 * 1.0), rtol=1e-9)
+
+
+def test_deform_single_sample_picks_nearest(oracle_mod):
+    """P = 1, K = 1, zero offsets, self-attention: every query reads its own value."""
+    rng = np.random.default_rng(51)
+    B, N, H, C = 1, 200, 2, 8
+    pos = rng.random((B, N, 2), dtype=np.float32)
+    off = np.zeros((B, N, H, 1, 1, 2), dtype=np.float32)
+    attn = np.ones((B, N, H, 1, 1), dtype=np.float32)
+    val = rng.standard_normal((B, N, H, C)).astype(np.float32)
+    out, idx = oracle_mod.deform(pos, pos, [0, N], off, attn, val, 1.0, 1, "shepard")
+    assert (idx[0, :, :, 0, 0, 0] == np.arange(N)[:, None]).all()
+    np.testing.assert_allclose(out[0], val[0] / (1 + 1e-8), rtol=1e-7)
+
+
+def test_deform_matches_knn_weights_gather_composition(oracle_mod):
+    """deform == per-sample brute-force knn + explicit weights + weighted_gather per head."""
+    rng = np.random.default_rng(52)
+    B, Nq, H, P, K, C = 1, 30, 2, 3, 4, 8
+    lv = [rng.random((B, 120, 2), dtype=np.float32), rng.random((B, 40, 2), dtype=np.float32)]
+    kv = np.concatenate(lv, 1)
+    ls = [0, 120, 160]
+    qp = rng.random((B, Nq, 2), dtype=np.float32)
+    off = (rng.standard_normal((B, Nq, H, 2, P, 2)) * 0.05).astype(np.float32)
+    at = rng.random((B, Nq, H, 2, P)).astype(np.float32)
+    val = rng.standard_normal((B, 160, H, C)).astype(np.float32)
+    for mode, pw in (("idw", 3.0), ("shepard", 1.5)):
+        out, _ = oracle_mod.deform(qp, kv, ls, off, at, val, pw, K, mode)
+        ref = np.zeros((B, Nq, H, C))
+        for h in range(H):
+            for l in range(2):
+                for p in range(P):
+                    loc = (qp + off[:, :, h, l, p]).astype(np.float32)
+                    ii, dd = oracle_mod.knn(loc, kv[:, ls[l]:ls[l + 1]], K)
+                    d = dd.astype(np.float64)
+                    if mode == "idw":
+                        u = 1 / (d ** pw + 1e-10)
+                        w = u / (u.sum(-1, keepdims=True) + 1e-12)
+                    else:
+                        e = np.exp(-pw * (np.sqrt(d) + 1e-6) - (-pw * (np.sqrt(d) + 1e-6)).max(-1, keepdims=True))
+                        w = e / (e.sum(-1, keepdims=True) + 1e-8)
+                    w = w * at[:, :, h, l, p][..., None]
+                    ref[:, :, h] += oracle_mod.weighted_gather(ii + ls[l], w, val[:, :, h])
+        np.testing.assert_allclose(out, ref, rtol=1e-6, atol=1e-7)
+
+
+def test_msdetrpc_and_sample_closed_forms(oracle_mod):
+    rng = np.random.default_rng(53)
+    B, N, M, K, Nv, C = 1, 20, 3, 4, 50, 8
+    idx = rng.integers(0, Nv, (B, N, M, K))
+    w = rng.random((B, N, M, K)).astype(np.float32)
+    a = rng.random((B, N, M)).astype(np.float32)
+    v = rng.standard_normal((B, Nv, C)).astype(np.float32)
+    out = oracle_mod.msdetrpc(idx, w, a, v)
+    ref = np.einsum("bnm,bnmk,bnmkc->bnc", a.astype(np.float64), w.astype(np.float64),
+                    v.astype(np.float64)[0][idx[0]][None])
+    np.testing.assert_allclose(out, ref, rtol=1e-6, atol=1e-7)
+    # sampling weights: eps placement of the two variants
+    sl = np.zeros((1, 1, 2), dtype=np.float32)
+    kv = np.array([[[0.0, 0.0], [3.0, 4.0]]], dtype=np.float32)
+    nb = np.array([[[0, 1]]])
+    w0, _ = oracle_mod.deform_sample(sl, kv, nb, 1.0, 0)
+    e = np.exp(-np.array([1e-6, 5 + 1e-6]) + 1e-6)
+    np.testing.assert_allclose(w0[0, 0], e / (e.sum() + 1e-8), rtol=1e-9)
+    w1, _ = oracle_mod.deform_sample(sl, kv, nb, 1.0, 1)
+    e = np.exp(-np.sqrt(np.array([1e-6, 25 + 1e-6])) + np.sqrt(1e-6))
+    np.testing.assert_allclose(w1[0, 0], e / (e.sum() + 1e-8), rtol=1e-9)
