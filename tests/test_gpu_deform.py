@@ -151,8 +151,10 @@ def test_msdetrpc(oracle_mod, dev, dtype):
     g = torch.Generator().manual_seed(5)
     B, N, M, K, Nv, C = 2, 200, 16, 3, 500, 32
     idx = torch.randint(0, Nv, (B, N, M, K), generator=g)
-    w = torch.rand((B, N, M, K), generator=g).to(dtype)
-    a = torch.rand((B, N, M), generator=g).to(dtype)
+    # softmaxed weights, as its callers pass (attention.py:381-399): outputs are
+    # convex combinations of the values
+    w = torch.softmax(torch.randn((B, N, M, K), generator=g), -1).to(dtype)
+    a = torch.softmax(torch.randn((B, N, M), generator=g), -1).to(dtype)
     v = torch.randn((B, Nv, C), generator=g).to(dtype)
     out = MSDETRPCFunction.apply(idx.to(dev), w.to(dev), a.to(dev), v.to(dev))
     _close(out, oracle_mod.msdetrpc(idx.numpy(), _np(w), _np(a), _np(v)), dtype)
