@@ -264,6 +264,7 @@ extern "C" aff_status aff_nbhd_attn_fwd(const aff_nbhd_attn_args *args, aff_stre
         AFF_CHECK_ARG(a.rel_width >= 1 && a.rel_width < 32768, "aff_nbhd_attn_fwd: rel_width %d", a.rel_width);
         AFF_CHECK_ARG(a.table_dtype >= 0 && a.table_dtype <= 2, "aff_nbhd_attn_fwd: table dtype");
     }
+    hipStream_t hs = static_cast<hipStream_t>(stream);
     attn::KernelFn fn = nullptr;
     if (a.dtype == AFF_F32) fn = attn::pick_d<float>(a.D, a.bias_mode);
     else if (a.dtype == AFF_BF16) fn = attn::pick_d<bf16_t>(a.D, a.bias_mode);
@@ -272,7 +273,6 @@ extern "C" aff_status aff_nbhd_attn_fwd(const aff_nbhd_attn_args *args, aff_stre
     const int64_t rows = (int64_t)a.B * a.H * a.N;
     const int64_t blocks = (rows + rows_per_block - 1) / rows_per_block;
     AFF_CHECK_ARG(blocks < (int64_t)1 << 31, "aff_nbhd_attn_fwd: problem too large");
-    hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(attn::THREADS), 0,
-                       static_cast<hipStream_t>(stream), a);
+    hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(attn::THREADS), 0, hs, a);
     return check_launch("aff_nbhd_attn_fwd");
 }
