@@ -23,7 +23,7 @@ AFF_ERR_LAUNCH = 4
 AFF_F32, AFF_F16, AFF_BF16 = 0, 1, 2
 DTYPE_CODE = {torch.float32: AFF_F32, torch.float16: AFF_F16, torch.bfloat16: AFF_BF16}
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 P = ctypes.c_void_p
 I32 = ctypes.c_int
@@ -52,6 +52,7 @@ class NbhdAttnArgs(ctypes.Structure):
         ("blank_k", P), ("blank_v", P),
         ("out", P), ("o_sb", I64), ("o_sh", I64), ("o_sn", I64),
         ("lse", P),
+        ("ws", P), ("ws_bytes", SZ),
     ]
 
 
@@ -81,6 +82,7 @@ SIGNATURES = {
     "aff_abi_version": (I32, []),
     "aff_knn_workspace_bytes": (SZ, [I32, I32, I32, I32, I32]),
     "aff_knn": (I32, [P, I64, I64, P, I64, I64, I32, I32, I32, I32, I32, P, I32, P, P, SZ, P]),
+    "aff_nbhd_attn_workspace_bytes": (SZ, [ctypes.POINTER(NbhdAttnArgs)]),
     "aff_nbhd_attn_fwd": (I32, [ctypes.POINTER(NbhdAttnArgs), P]),
     "aff_weighted_features_fwd": (I32, [P, I32, I64, I64, I64, I64, P, I32, I64, I64, P, I32, I64, I64,
                                         I32, I32, I32, I32, I32, I32, P, I64, I64, I64, P]),

@@ -21,4 +21,4 @@ void clear_error() { g_last_error[0] = '\0'; }
 
 extern "C" const char *aff_last_error(void) { return aff::g_last_error; }
 
-extern "C" int aff_abi_version(void) { return 2; }
+extern "C" int aff_abi_version(void) { return 3; }

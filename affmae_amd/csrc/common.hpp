@@ -34,12 +34,9 @@ struct f16_t { _Float16 v; };
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
     return __uint_as_float(uint32_t(b) << 16);
 }
-// Round to nearest even; NaN stays a quiet NaN.
+// Round to nearest even (gfx950's v_cvt_pk_bf16_f32); NaN stays a NaN.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return uint16_t(u >> 16);
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 // Element-type traits: storage type, vector load of 8 elements into fp32.
@@ -155,6 +152,29 @@ __device__ __forceinline__ float xor_lane(float v) {
     }
 }
 
+// Data-parallel-primitive move with a compile-time control word.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+// Max / sum over each aligned row of 16 lanes, result in every lane of the
+// row: two quad butterflies (quad_perm [1,0,3,2] and [2,3,0,1]) leave each
+// lane with its quad's value, then row rotations by 4 and 8 fold in the other
+// three quads.  All DPP, no LDS-unit permutes.
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_mov<0xB1>(v));
+    v = fmaxf(v, dpp_mov<0x4E>(v));
+    v = fmaxf(v, dpp_mov<0x124>(v));
+    return fmaxf(v, dpp_mov<0x128>(v));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_mov<0xB1>(v);
+    v += dpp_mov<0x4E>(v);
+    v += dpp_mov<0x124>(v);
+    return v + dpp_mov<0x128>(v);
+}
+
 // Sum over aligned groups of G lanes (G a power of two <= 64).
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
@@ -165,6 +185,14 @@ __device__ __forceinline__ float group_sum(float v) {
     if constexpr (G >= 32) v += xor_lane<16>(v);
     if constexpr (G >= 64) v += xor_lane<32>(v);
     return v;
+}
+
+// Workgroup barrier for kernels whose threads communicate only through LDS:
+// waits for this wave's LDS operations, not for its global loads (which
+// __syncthreads() also drains), so prefetched global data stays in flight
+// across the barrier.  Global results read by other threads need __syncthreads().
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 // Map a linear block id so that consecutive work items stay on one XCD.

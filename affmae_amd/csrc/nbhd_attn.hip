@@ -6,21 +6,44 @@
 // blank token joins the softmax after the neighbours, the running maximum
 // starts at -1e11 and LSE = m + log(l + 1e-12).
 //
-// Layout: D/8 lanes own one (b, h, n) row; each lane holds 8 channels of q
-// and of the accumulator.  Neighbours are consumed in blocks of 8: the 8
-// index/mask/bias values and the 16 K/V row pieces are loaded before use so
-// up to 16 gathers per lane are in flight, then one online-softmax rescale
-// is applied per block.  Work is ordered (b, h, n) with n fastest and the
-// block order is swizzled so each XCD walks a contiguous range: the K/V
-// planes of one (b, h) (N * D * 4 bytes in bf16) stay resident in that XCD's
-// L2 while its neighbour gathers run.
+// Two kernels implement it.
+//
+// nbhd_attn_tile_kernel (bf16 / fp16, head_dim 32, M <= 64): one workgroup
+// takes 16 consecutive queries of one image and every head.  The tile's
+// neighbour indices are deduplicated into a "union" of at most 256 token
+// rows (an LDS bitmap over the tile's index window plus a popcount prefix
+// gives every (query, neighbour) pair a union slot).  Per head the union's
+// K rows feed S^T = K_u Q^T on v_mfma_f32_16x16x32 (K straight from HBM/L2
+// into the A operand, Q as the B operand), S goes to LDS, the softmax runs
+// in (query, neighbour) layout - 16 lanes per query, four entries per lane -
+// and the probabilities are scattered into a dense P[16 x U] tile, zero where
+// a query does not use a union row.  O = P V_u is a second MFMA pass with V
+// staged transposed in LDS.  Every K/V row the tile touches is read once per
+// head instead of once per (query, neighbour), and both contractions run on
+// the matrix cores.  The next head's K/V/Q/bias loads are issued as soon as
+// the current head's K/V registers are consumed (after its S MFMAs and V^T
+// stores), so their latency overlaps its softmax, PV pass and store.  A tile
+// whose union exceeds 256 rows, whose index window exceeds 8192, whose
+// neighbour lists repeat an index within one query, or whose mask differs per
+// head is flagged in the caller's workspace (one byte per tile) and computed
+// by nbhd_attn_tile_fallback_kernel, launched right after on the same stream,
+// with the per-row routine below.
+//
+// nbhd_attn_fwd_kernel (every dtype and head_dim): D/8 lanes own one
+// (b, h, n) row (8 channels each).  Neighbours are consumed 8 at a time:
+// indices, mask, bias and 16 K/V row pieces are loaded before use, then one
+// online-softmax rescale is applied per block.
+//
+// Both kernels swizzle their block order so each XCD walks a contiguous
+// range of images and keeps that image's K/V planes in its own L2.
 #include "common.hpp"
+
+#include <limits.h>
 
 namespace aff {
 namespace attn {
 
 constexpr int THREADS = 256;
-constexpr int NB = 8;  // neighbours per online-softmax block
 constexpr float MASKED_LOGIT = -1e11f;
 
 __device__ __forceinline__ int64_t load_index(const void *p, int is_i64, int64_t i) {
@@ -39,21 +62,22 @@ __device__ __forceinline__ int64_t pe_from_coords(float qx, float qy, float mx, 
     return (int64_t)(ry * T + rx);
 }
 
-template <typename T, int D, int BIAS>
-__global__ __launch_bounds__(THREADS) void nbhd_attn_fwd_kernel(const aff_nbhd_attn_args a) {
+// Continuous relative-position features f(dx, dy) = (dx, dy, r, dy/r, dx/r).
+__device__ __forceinline__ float cont_bias(const float *pw, float pb, float dx, float dy) {
+    const float r = sqrtf(dx * dx + dy * dy);
+    const float sn = r > 0.f ? dy / r : 0.f, cs = r > 0.f ? dx / r : 0.f;
+    return pb + pw[0] * dx + pw[1] * dy + pw[2] * r + pw[3] * sn + pw[4] * cs;
+}
+
+// ------------------------------------------------------------------------
+// Per-row routine: LPR = D/8 aligned lanes compute one (b, h, n) output row,
+// NB neighbours per online-softmax block.
+// ------------------------------------------------------------------------
+template <typename T, int D, int BIAS, int NB>
+__device__ __forceinline__ void attend_row(const aff_nbhd_attn_args &a, int b, int h, int n, int sub) {
     using IO = ElemIO<T>;
     constexpr int LPR = D / 8;
-    constexpr int ROWS = THREADS / LPR;
-    const uint32_t bid = xcd_swizzle(blockIdx.x, gridDim.x);
-    const int sub = threadIdx.x % LPR;
-    const int64_t row = (int64_t)bid * ROWS + threadIdx.x / LPR;
-    const int64_t total = (int64_t)a.B * a.H * a.N;
-    if (row >= total) return;  // whole lane groups leave together
     const int N = a.N, M = a.M, H = a.H;
-    const int n = int(row % N);
-    const int64_t bh = row / N;
-    const int h = int(bh % H);
-    const int b = int(bh / H);
 
     const T *Kb = static_cast<const T *>(a.k) + (int64_t)b * a.k_sb + (int64_t)h * a.k_sh + sub * 8;
     const T *Vb = static_cast<const T *>(a.v) + (int64_t)b * a.v_sb + (int64_t)h * a.v_sh + sub * 8;
@@ -125,10 +149,7 @@ __global__ __launch_bounds__(THREADS) void nbhd_attn_fwd_kernel(const aff_nbhd_a
                 if (pe >= 0 && pe < a.table_rows) bias[u] = load_any(a.table, a.table_dtype, pe * H + h);
             } else if constexpr (BIAS == 3) {
                 const float mx = pos_b[idx[u] * a.pos_sn], my = pos_b[idx[u] * a.pos_sn + 1];
-                const float dx = mx - pqx, dy = my - pqy;
-                const float r = sqrtf(dx * dx + dy * dy);
-                const float sn = r > 0.f ? dy / r : 0.f, cs = r > 0.f ? dx / r : 0.f;
-                bias[u] = pb + pw[0] * dx + pw[1] * dy + pw[2] * r + pw[3] * sn + pw[4] * cs;
+                bias[u] = cont_bias(pw, pb, mx - pqx, my - pqy);
             } else if constexpr (BIAS == 4) {
                 const float mx = pos_b[idx[u] * a.pos_sn], my = pos_b[idx[u] * a.pos_sn + 1];
                 const int64_t pe = pe_from_coords(pqx, pqy, mx, my, relW, relT);
@@ -192,7 +213,425 @@ __global__ __launch_bounds__(THREADS) void nbhd_attn_fwd_kernel(const aff_nbhd_a
     IO::store8(static_cast<T *>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh +
                    (int64_t)n * a.o_sn + sub * 8,
                o);
-    if (a.lse && sub == 0) a.lse[row] = lse;
+    if (a.lse && sub == 0) a.lse[((int64_t)b * H + h) * N + n] = lse;
+}
+
+template <typename T, int D, int BIAS>
+__global__ __launch_bounds__(THREADS) void nbhd_attn_fwd_kernel(const aff_nbhd_attn_args a) {
+    constexpr int LPR = D / 8;
+    constexpr int ROWS = THREADS / LPR;
+    const uint32_t bid = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int sub = threadIdx.x % LPR;
+    const int64_t row = (int64_t)bid * ROWS + threadIdx.x / LPR;
+    const int64_t total = (int64_t)a.B * a.H * a.N;
+    if (row >= total) return;  // whole lane groups leave together
+    const int n = int(row % a.N);
+    const int64_t bh = row / a.N;
+    attend_row<T, D, BIAS, 8>(a, int(bh / a.H), int(bh % a.H), n, sub);
+}
+
+// ------------------------------------------------------------------------
+// MFMA tile kernel
+// ------------------------------------------------------------------------
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T> struct Mfma;
+template <> struct Mfma<bf16_t> {
+    typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+    __device__ __forceinline__ static f32x4 mma(uint4 a, uint4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0,
+                                                       0, 0);
+    }
+    __device__ __forceinline__ static uint16_t from_f32(float x) { return f32_to_bf16(x); }
+    __device__ __forceinline__ static float to_f32(uint16_t x) { return bf16_to_f32(x); }
+};
+template <> struct Mfma<f16_t> {
+    typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+    __device__ __forceinline__ static f32x4 mma(uint4 a, uint4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0, 0,
+                                                      0);
+    }
+    __device__ __forceinline__ static uint16_t from_f32(float x) { return __builtin_bit_cast(uint16_t, _Float16(x)); }
+    __device__ __forceinline__ static float to_f32(uint16_t x) { return float(__builtin_bit_cast(_Float16, x)); }
+};
+
+namespace tile {
+constexpr int TQ = 16;               // queries per workgroup (MFMA rows)
+constexpr int HD = 32;               // head_dim of this kernel
+constexpr int UMAX = 256;            // union rows held in LDS
+constexpr int WWORDS = 256;          // index-window bitmap words: windows up to 8192 indices
+constexpr int MAXM = 64;             // neighbours per query
+constexpr int RJ = MAXM / 16;        // neighbour entries per lane (16 lanes per query)
+constexpr int KBW = UMAX / 64;       // 16-row K blocks per wave
+constexpr int PCI = (UMAX * 2 + THREADS - 1) / THREADS;  // V slot-pair chunks per thread
+constexpr int SP = UMAX + 4;         // S row pitch (fp32): 16-byte rows, 4-bank shift per row
+constexpr int PP = UMAX + 8;         // P row pitch (16-bit): 16-byte rows, column UMAX is a dummy
+constexpr int VP = UMAX + 4;         // V^T row pitch (16-bit): 8-byte rows, conflict-free pair stores
+static_assert(WWORDS == THREADS, "one bitmap word per thread");
+static_assert(UMAX % 32 == 0 && (VP / 2) % 8 == 2, "V^T pitch keeps the pair stores conflict-free");
+}  // namespace tile
+
+__device__ __forceinline__ uint4 ld16(const char *p) { return *reinterpret_cast<const uint4 *>(p); }
+__device__ __forceinline__ uint32_t ld4(const char *p) { return *reinterpret_cast<const uint32_t *>(p); }
+
+// One workgroup per 16-query tile.  flags[tile] = 0 when the tile ran here,
+// 1 when its union does not fit (the fallback kernel then computes it).
+template <typename T, int BIAS>
+__global__ __launch_bounds__(THREADS) void nbhd_attn_tile_kernel(const aff_nbhd_attn_args a) {
+    using namespace tile;
+    using MM = Mfma<T>;
+    struct SetupLds {
+        uint32_t bits[WWORDS];
+        uint32_t pref[WWORDS];
+    };
+    __shared__ __align__(16) union {
+        SetupLds s;
+        float S[TQ * SP];
+    } sh;
+    __shared__ __align__(16) uint16_t Pb[TQ * PP];
+    __shared__ __align__(16) uint16_t VT[HD * VP];
+    __shared__ __align__(16) float Ob[2][TQ][HD];
+    __shared__ int ulist[UMAX];
+    __shared__ uint32_t qbits[TQ][UMAX / 32];
+    __shared__ float linfo[TQ][2];
+    __shared__ int red[4];
+
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int q = t >> 4, jl = t & 15;
+    const int N = a.N, M = a.M, H = a.H;
+    const int tiles = (N + TQ - 1) / TQ;
+    const uint32_t bid = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int b = int(bid / tiles);
+    const int n0 = int(bid % tiles) * TQ;
+    const int n = n0 + q;
+    const bool qlive = n < N;
+    const int nc = min(n, N - 1);
+    const int rowq = lane & 15, grp = lane >> 4;
+
+    if (t < 4) red[t] = 0;
+    sh.s.bits[t] = 0;
+    if (t < TQ * UMAX / 32) (&qbits[0][0])[t] = 0;
+    for (int i = t; i < TQ * PP / 2; i += THREADS) reinterpret_cast<uint32_t *>(Pb)[i] = 0;
+
+    // ---- this lane's (query, neighbour) entries: j = jl + 16 r.  With a mask,
+    // the head-0 row is every head's row (a per-head mask sends the tile to the
+    // fallback kernel).
+    const int64_t mi_row = (int64_t)b * a.mi_sb + (int64_t)nc * a.mi_sn;
+    const int64_t mk_row = (int64_t)b * a.mask_sb + (int64_t)nc * a.mask_sn;
+    int idx[RJ];
+    bool use[RJ];
+    int nmask = 0;
+#pragma unroll
+    for (int r = 0; r < RJ; ++r) {
+        const int j = jl + 16 * r;
+        const bool live = qlive && j < M;
+        const int64_t ix = live ? load_index(a.member_idx, a.idx_is_i64, mi_row + j) : -1;
+        bool ok = live && ix >= 0 && ix < N;
+        if (ok && a.mask) ok = a.mask[mk_row + j] != 0;
+        use[r] = ok;
+        idx[r] = ok ? int(ix) : 0;
+        nmask += (live && !ok) ? 1 : 0;
+    }
+    // coordinate terms of the bias, shared by every head (modes 3 and 4)
+    float fx[RJ], fy[RJ];
+    int tab[RJ];
+#pragma unroll
+    for (int r = 0; r < RJ; ++r) {
+        fx[r] = fy[r] = 0.f;
+        tab[r] = -1;
+    }
+    if constexpr (BIAS == 2) {
+#pragma unroll
+        for (int r = 0; r < RJ; ++r)
+            if (use[r]) {
+                const int64_t v =
+                    load_index(a.pe_idx, a.pe_is_i64, (int64_t)b * a.pe_sb + (int64_t)nc * a.pe_sn + jl + 16 * r);
+                tab[r] = (v >= 0 && v < a.table_rows) ? int(v) : -1;
+            }
+    } else if constexpr (BIAS == 3 || BIAS == 4) {
+        const float *pos_b = a.pos + (int64_t)b * a.pos_sb;
+        const float pqx = pos_b[(int64_t)nc * a.pos_sn], pqy = pos_b[(int64_t)nc * a.pos_sn + 1];
+        const float relW = float(a.rel_width), relT = float(2 * a.rel_width + 1);
+#pragma unroll
+        for (int r = 0; r < RJ; ++r)
+            if (use[r]) {
+                const float mx = pos_b[(int64_t)idx[r] * a.pos_sn], my = pos_b[(int64_t)idx[r] * a.pos_sn + 1];
+                if constexpr (BIAS == 4) {
+                    const int64_t v = pe_from_coords(pqx, pqy, mx, my, relW, relT);
+                    tab[r] = (v >= 0 && v < a.table_rows) ? int(v) : -1;
+                } else {
+                    fx[r] = mx - pqx;
+                    fy[r] = my - pqy;
+                }
+            }
+    }
+
+    // ---- union of the tile's neighbour rows over the index window
+    // [wlo, wlo + 8192) around the tile (every index when N <= 8192); an index
+    // outside it, or a mask that differs per head, flags the tile
+    const int wlo = max(0, min(n0 + TQ / 2 - WWORDS * 16, N - WWORDS * 32));
+    bool outside = false;
+#pragma unroll
+    for (int r = 0; r < RJ; ++r)
+        if (use[r]) {
+            const unsigned o = unsigned(idx[r] - wlo);
+            if (o < unsigned(WWORDS * 32)) atomicOr(&sh.s.bits[o >> 5], 1u << (o & 31));
+            else outside = true;
+        }
+    if (outside) red[0] = 1;
+    uint8_t *flags = static_cast<uint8_t *>(a.ws);
+    lds_barrier();
+    if ((a.mask && a.mask_sh != 0) || red[0]) {
+        if (t == 0) flags[bid] = 1;
+        return;
+    }
+    if (w == 0) {
+        uint32_t c[4];
+        int tot = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            c[i] = __popc(sh.s.bits[lane * 4 + i]);
+            tot += c[i];
+        }
+        int inc = tot;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(inc, o, 64);
+            if (lane >= o) inc += v;
+        }
+        int ex = inc - tot;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sh.s.pref[lane * 4 + i] = ex;
+            ex += c[i];
+        }
+        if (lane == 63) red[2] = inc;
+    }
+    lds_barrier();
+    const int U = red[2];
+    if (U > UMAX) {
+        if (t == 0) flags[bid] = 1;
+        return;
+    }
+    int slot[RJ];
+#pragma unroll
+    for (int r = 0; r < RJ; ++r) {
+        slot[r] = UMAX;  // the dummy column
+        if (use[r]) {
+            const int o = idx[r] - wlo, wd = o >> 5, bt = o & 31;
+            const int s = int(sh.s.pref[wd] + __popc(sh.s.bits[wd] & ((1u << bt) - 1u)));
+            slot[r] = s;
+            ulist[s] = idx[r];
+            const uint32_t bit = 1u << (s & 31);
+            if (atomicOr(&qbits[q][s >> 5], bit) & bit) red[3] = 1;  // repeated index
+        }
+    }
+    lds_barrier();
+    if (red[3]) {
+        if (t == 0) flags[bid] = 1;
+        return;
+    }
+    if (t == 0) flags[bid] = 0;
+
+    const int Up = (U + 31) & ~31;
+    const int nkb = Up >> 4, nkb2 = Up >> 5;
+    const bool blank = a.blank_k != nullptr;
+    const float scale = a.scale;
+    const int nm = nmask;
+
+    // ---- per-lane byte offsets into one head's planes, the same for every head
+    // (the host guarantees they fit in 32 bits).  Union slots past U read the
+    // first union row: their S columns are never read and their P columns stay
+    // zero.  Unused entries read S and write P in the dummy column UMAX.
+    const int row0 = U > 0 ? ulist[0] : 0;
+    const uint32_t ksn2 = uint32_t(a.k_sn * 2), vsn2 = uint32_t(a.v_sn * 2);  // < 2^24, host-checked
+    uint32_t koff[KBW];
+#pragma unroll
+    for (int i = 0; i < KBW; ++i) {
+        const int s = (w + 4 * i) * 16 + rowq;
+        koff[i] = __umul24(uint32_t(s < U ? ulist[s] : row0), ksn2) + grp * 16;
+    }
+    uint32_t voff[PCI][2];
+#pragma unroll
+    for (int i = 0; i < PCI; ++i) {
+        const int pc = t + THREADS * i, s = 2 * (pc >> 2), dc = pc & 3;
+        voff[i][0] = __umul24(uint32_t(s < U ? ulist[s] : row0), vsn2) + dc * 16;
+        voff[i][1] = __umul24(uint32_t(s + 1 < U ? ulist[s + 1] : row0), vsn2) + dc * 16;
+    }
+    const uint32_t qoff = uint32_t(((int64_t)min(n0 + rowq, N - 1) * a.q_sn + grp * 8) * 2);
+    const uint32_t qpoff = uint32_t(((int64_t)nc * a.q_sn + 2 * jl) * 2);
+    int sidx[RJ], pidx[RJ];
+#pragma unroll
+    for (int r = 0; r < RJ; ++r) {
+        sidx[r] = q * SP + slot[r];
+        pidx[r] = q * PP + slot[r];
+    }
+    const float *table = static_cast<const float *>(a.table);
+    const int64_t brow = (int64_t)b * a.bias_sb + (int64_t)nc * a.bias_sn;
+    const char *qb = static_cast<const char *>(a.q) + (int64_t)b * a.q_sb * 2;
+    const char *kb_ = static_cast<const char *>(a.k) + (int64_t)b * a.k_sb * 2;
+    const char *vb = static_cast<const char *>(a.v) + (int64_t)b * a.v_sb * 2;
+    const int64_t qsh = a.q_sh * 2, ksh = a.k_sh * 2, vsh = a.v_sh * 2;
+
+    // ---- registers of one head, loaded one head ahead
+    uint4 qf, kf[KBW], vr[PCI][2];
+    uint32_t qpair = 0, bkpair = 0, bvpair = 0;
+    float bs[RJ];
+    auto load_head = [&](int h) {
+        const char *Qh = qb + h * qsh, *Kh = kb_ + h * ksh, *Vh = vb + h * vsh;
+        qf = ld16(Qh + qoff);  // B operand of S^T = K_u Q^T: query rowq, channels 8*grp .. +8
+        if (blank) {
+            qpair = ld4(Qh + qpoff);
+            bkpair = ld4(static_cast<const char *>(a.blank_k) + (h * HD + 2 * jl) * 2);
+            bvpair = ld4(static_cast<const char *>(a.blank_v) + (h * HD + 2 * jl) * 2);
+        }
+#pragma unroll
+        for (int i = 0; i < KBW; ++i)
+            if (w + 4 * i < nkb) kf[i] = ld16(Kh + koff[i]);  // A operand: union row, channels 8*grp .. +8
+#pragma unroll
+        for (int i = 0; i < PCI; ++i)
+            if (32 * w + 128 * i < Up) {  // this wave's slot range [32w + 128i, +32) is in use
+                vr[i][0] = ld16(Vh + voff[i][0]);
+                vr[i][1] = ld16(Vh + voff[i][1]);
+            }
+        // raw values: the selects wait until use, so these loads stay in flight
+#pragma unroll
+        for (int r = 0; r < RJ; ++r) {
+            if constexpr (BIAS == 1) {
+                bs[r] = load_any(a.bias, a.bias_dtype, brow + (int64_t)h * a.bias_sh + jl + 16 * r);
+            } else if constexpr (BIAS == 2 || BIAS == 4) {
+                bs[r] = table[(tab[r] >= 0 ? tab[r] : 0) * H + h];
+            } else if constexpr (BIAS == 3) {
+                const float *pw = a.pos_w + h * 5;
+                bs[r] = cont_bias(pw, a.pos_b[h], fx[r], fy[r]);
+            } else {
+                bs[r] = 0.f;
+            }
+        }
+    };
+
+    load_head(0);
+    for (int h = 0; h < H; ++h) {
+        // V^T from the prefetched slot pairs: one 32-bit store per channel
+#pragma unroll
+        for (int i = 0; i < PCI; ++i)
+            if (32 * w + 128 * i < Up) {
+                const int pc = t + THREADS * i, s = 2 * (pc >> 2), dc = pc & 3;
+                const uint32_t x[4] = {vr[i][0].x, vr[i][0].y, vr[i][0].z, vr[i][0].w};
+                const uint32_t y[4] = {vr[i][1].x, vr[i][1].y, vr[i][1].z, vr[i][1].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    *reinterpret_cast<uint32_t *>(&VT[(dc * 8 + 2 * e) * VP + s]) =
+                        __builtin_amdgcn_perm(y[e], x[e], 0x05040100u);
+                    *reinterpret_cast<uint32_t *>(&VT[(dc * 8 + 2 * e + 1) * VP + s]) =
+                        __builtin_amdgcn_perm(y[e], x[e], 0x07060302u);
+                }
+            }
+        // S^T blocks -> S[query][slot]
+#pragma unroll
+        for (int i = 0; i < KBW; ++i)
+            if (w + 4 * i < nkb) {
+                const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                const f32x4 sv = MM::mma(kf[i], qf, z);
+                *reinterpret_cast<f32x4 *>(&sh.S[rowq * SP + (w + 4 * i) * 16 + 4 * grp]) = sv;
+            }
+        const uint32_t qp = qpair, bkp = bkpair, bvp = bvpair;
+        float bcur[RJ];
+#pragma unroll
+        for (int r = 0; r < RJ; ++r) bcur[r] = bs[r];  // selected at use: the entry's mask or table row
+        // this head's K/V registers are consumed: the next head's loads now have the
+        // whole softmax, PV pass and store of this head to arrive
+        if (h + 1 < H) load_head(h + 1);
+        lds_barrier();
+
+        // ---- softmax in (query, neighbour) layout: 16 lanes per query
+        float s_[RJ];
+        float mloc = MASKED_LOGIT;
+#pragma unroll
+        for (int r = 0; r < RJ; ++r) {
+            float bias = bcur[r];
+            if constexpr (BIAS == 2 || BIAS == 4) bias = tab[r] >= 0 ? bias : 0.f;
+            const float v = sh.S[sidx[r]] * scale + bias;
+            s_[r] = use[r] ? v : -INFINITY;
+            mloc = fmaxf(mloc, s_[r]);
+        }
+        float sb = 0.f;
+        if (blank) {
+            const float part = MM::to_f32(uint16_t(qp & 0xffffu)) * MM::to_f32(uint16_t(bkp & 0xffffu)) +
+                               MM::to_f32(uint16_t(qp >> 16)) * MM::to_f32(uint16_t(bkp >> 16));
+            sb = row16_sum(part) * scale;
+            mloc = fmaxf(mloc, sb);
+        }
+        const float m = row16_max(mloc);
+        float lsum = nm ? float(nm) * __expf(MASKED_LOGIT - m) : 0.f;
+#pragma unroll
+        for (int r = 0; r < RJ; ++r) {
+            const float p = __expf(s_[r] - m);
+            lsum += p;
+            Pb[pidx[r]] = MM::from_f32(p);
+        }
+        const float pblank = blank ? __expf(sb - m) : 0.f;
+        const float l = row16_sum(lsum) + pblank;
+        if (jl == 0) {
+            linfo[q][0] = __builtin_amdgcn_rcpf(l + 1e-12f);  // 1 ulp: outputs are 16-bit
+            linfo[q][1] = pblank;
+            if (a.lse && qlive) a.lse[((int64_t)b * H + h) * N + n] = m + __logf(l + 1e-12f);
+        }
+        lds_barrier();
+
+        // ---- O = P V_u.  Wave w: channel half (w & 1), 32-slot blocks of parity (w >> 1).
+        {
+            const int hd = w & 1;
+            f32x4 o = {0.f, 0.f, 0.f, 0.f};
+            for (int kb2 = w >> 1; kb2 < nkb2; kb2 += 2) {
+                const int col = kb2 * 32 + 8 * grp;
+                const uint4 pa = *reinterpret_cast<const uint4 *>(&Pb[rowq * PP + col]);
+                const uint2 va = *reinterpret_cast<const uint2 *>(&VT[(rowq + 16 * hd) * VP + col]);
+                const uint2 vb2 = *reinterpret_cast<const uint2 *>(&VT[(rowq + 16 * hd) * VP + col + 4]);
+                o = MM::mma(pa, make_uint4(va.x, va.y, vb2.x, vb2.y), o);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) Ob[w >> 1][4 * grp + i][rowq + 16 * hd] = o[i];
+        }
+        lds_barrier();
+
+        // ---- two partial sums, blank value, normalise, store
+        {
+            const int d0 = 2 * jl;
+            const float2 p0 = *reinterpret_cast<const float2 *>(&Ob[0][q][d0]);
+            const float2 p1 = *reinterpret_cast<const float2 *>(&Ob[1][q][d0]);
+            const float pbv = linfo[q][1], inv = linfo[q][0];
+            float x0 = p0.x + p1.x, x1 = p0.y + p1.y;
+            if (blank) {
+                x0 += pbv * MM::to_f32(uint16_t(bvp & 0xffffu));
+                x1 += pbv * MM::to_f32(uint16_t(bvp >> 16));
+            }
+            const uint32_t packed = uint32_t(MM::from_f32(x0 * inv)) | (uint32_t(MM::from_f32(x1 * inv)) << 16);
+            if (qlive)
+                *reinterpret_cast<uint32_t *>(static_cast<T *>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh +
+                                              (int64_t)n * a.o_sn + d0) = packed;
+        }
+        // The next head's first LDS writes (V^T, S) touch regions whose last readers
+        // (PV, softmax) finished before the barrier above; its Ob / linfo writes come
+        // after its own first barrier, which every lane reaches only after this store.
+    }
+}
+
+// The tiles the MFMA kernel flagged: their 16 x H rows through the per-row routine.
+template <typename T, int BIAS>
+__global__ __launch_bounds__(THREADS) void nbhd_attn_tile_fallback_kernel(const aff_nbhd_attn_args a, int ntiles) {
+    using namespace tile;
+    const uint8_t *flags = static_cast<const uint8_t *>(a.ws);
+    const int tiles = (a.N + TQ - 1) / TQ;
+    const int sub = threadIdx.x & 3, rr = threadIdx.x >> 2;
+    for (int tl = blockIdx.x; tl < ntiles; tl += gridDim.x) {
+        if (!flags[tl]) continue;
+        const int b = tl / tiles, n0 = (tl % tiles) * TQ;
+        for (int p = rr; p < TQ * a.H; p += THREADS / 4) {
+            const int qq = p % TQ, h = p / TQ;
+            if (n0 + qq < a.N) attend_row<T, HD, BIAS, 8>(a, b, h, n0 + qq, sub);
+        }
+    }
 }
 
 using KernelFn = void (*)(const aff_nbhd_attn_args);
@@ -220,12 +659,58 @@ KernelFn pick_d(int D, int mode) {
     }
 }
 
+template <typename T>
+KernelFn pick_tile(int mode) {
+    switch (mode) {
+        case 0: return nbhd_attn_tile_kernel<T, 0>;
+        case 1: return nbhd_attn_tile_kernel<T, 1>;
+        case 2: return nbhd_attn_tile_kernel<T, 2>;
+        case 3: return nbhd_attn_tile_kernel<T, 3>;
+        default: return nbhd_attn_tile_kernel<T, 4>;
+    }
+}
+
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+using FallbackFn = void (*)(const aff_nbhd_attn_args, int);
+
+template <typename T>
+FallbackFn pick_fallback(int mode) {
+    switch (mode) {
+        case 0: return nbhd_attn_tile_fallback_kernel<T, 0>;
+        case 1: return nbhd_attn_tile_fallback_kernel<T, 1>;
+        case 2: return nbhd_attn_tile_fallback_kernel<T, 2>;
+        case 3: return nbhd_attn_tile_fallback_kernel<T, 3>;
+        default: return nbhd_attn_tile_fallback_kernel<T, 4>;
+    }
+}
+
+// The MFMA tile path takes 16-bit q/k/v with head_dim 32, up to 64 neighbours,
+// an fp32 bias table (modes 2 and 4), and row byte offsets inside one (b, h)
+// plane that fit the kernel's 32-bit offsets.
+inline bool use_tile_path(const aff_nbhd_attn_args &a) {
+    if (a.dtype == AFF_F32 || a.D != tile::HD || a.M > tile::MAXM) return false;
+    if ((a.bias_mode == 2 || a.bias_mode == 4) && a.table_dtype != AFF_F32) return false;
+    // 32-bit byte offsets built with 24-bit multiplies: row index and row stride in bytes below 2^24
+    auto plane_ok = [&](int64_t sn) {
+        return sn >= 0 && sn * 2 < ((int64_t)1 << 24) && ((int64_t)(a.N - 1) * sn + a.D) * 2 < ((int64_t)1 << 32);
+    };
+    return a.N < (1 << 24) && plane_ok(a.q_sn) && plane_ok(a.k_sn) && plane_ok(a.v_sn);
+}
+
+inline int64_t tile_count(const aff_nbhd_attn_args &a) {
+    return (int64_t)a.B * ((a.N + tile::TQ - 1) / tile::TQ);
+}
 
 }  // namespace attn
 }  // namespace aff
 
 using namespace aff;
+
+extern "C" size_t aff_nbhd_attn_workspace_bytes(const aff_nbhd_attn_args *args) {
+    if (args == nullptr || (int64_t)args->B * args->H * args->N == 0) return 0;
+    return attn::use_tile_path(*args) ? (size_t)attn::tile_count(*args) : 0;
+}
 
 extern "C" aff_status aff_nbhd_attn_fwd(const aff_nbhd_attn_args *args, aff_stream_t stream) {
     AFF_CHECK_ARG(args != nullptr, "aff_nbhd_attn_fwd: NULL args");
@@ -265,6 +750,25 @@ extern "C" aff_status aff_nbhd_attn_fwd(const aff_nbhd_attn_args *args, aff_stre
         AFF_CHECK_ARG(a.table_dtype >= 0 && a.table_dtype <= 2, "aff_nbhd_attn_fwd: table dtype");
     }
     hipStream_t hs = static_cast<hipStream_t>(stream);
+
+    if (attn::use_tile_path(a)) {
+        const int64_t ntiles = attn::tile_count(a);
+        AFF_CHECK_ARG(ntiles < (int64_t)1 << 31, "aff_nbhd_attn_fwd: problem too large");
+        if (a.ws == nullptr || a.ws_bytes < (size_t)ntiles)
+            return fail(AFF_ERR_WORKSPACE, "aff_nbhd_attn_fwd: workspace of %lld bytes needed (got %zu)",
+                        (long long)ntiles, a.ws ? a.ws_bytes : (size_t)0);
+        const bool bf = a.dtype == AFF_BF16;
+        hipLaunchKernelGGL(bf ? attn::pick_tile<bf16_t>(a.bias_mode) : attn::pick_tile<f16_t>(a.bias_mode),
+                           dim3((unsigned)ntiles), dim3(attn::THREADS), 0, hs, a);
+        aff_status st = check_launch("aff_nbhd_attn_fwd (tiles)");
+        if (st != AFF_OK) return st;
+        // flagged tiles: a grid-stride pass whose blocks skip unflagged tiles
+        const int fb = (int)(ntiles < 2048 ? ntiles : 2048);
+        hipLaunchKernelGGL(bf ? attn::pick_fallback<bf16_t>(a.bias_mode) : attn::pick_fallback<f16_t>(a.bias_mode),
+                           dim3(fb), dim3(attn::THREADS), 0, hs, a, (int)ntiles);
+        return check_launch("aff_nbhd_attn_fwd (flagged tiles)");
+    }
+
     attn::KernelFn fn = nullptr;
     if (a.dtype == AFF_F32) fn = attn::pick_d<float>(a.D, a.bias_mode);
     else if (a.dtype == AFF_BF16) fn = attn::pick_d<bf16_t>(a.D, a.bias_mode);

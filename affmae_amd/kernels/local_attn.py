@@ -116,8 +116,7 @@ def nbhd_attn_fwd(q, k, v, member_idx, scale, *, bias=None, pe_idx=None, pe_tabl
         assert pe_table is not None and pe_table.dim() == 2 and pe_table.shape[1] == H, \
             "pe_table must be [rows, H]"
         assert tuple(pe_idx.shape) == (B, N, M), "pe_idx must be [B,N,M]"
-        tb = pe_table if pe_table.dtype in _lib.DTYPE_CODE else pe_table.to(torch.float32)
-        tb = tb.contiguous()
+        tb = pe_table.detach().to(torch.float32).contiguous()   # [T*T, H], ~1 MB: the fast path reads fp32
         pe = _idx(pe_idx)
         a.bias_mode = 2
         a.pe_idx, a.pe_is_i64 = pe.data_ptr(), 1 if pe.dtype == torch.int64 else 0
@@ -127,8 +126,7 @@ def nbhd_attn_fwd(q, k, v, member_idx, scale, *, bias=None, pe_idx=None, pe_tabl
     elif pos is not None and pe_table is not None:
         assert pe_table.dim() == 2 and pe_table.shape[1] == H, "pe_table must be [rows, H]"
         assert tuple(pos.shape) == (B, N, 2), "pos must be [B,N,2]"
-        tb = pe_table if pe_table.dtype in _lib.DTYPE_CODE else pe_table.to(torch.float32)
-        tb = tb.contiguous()
+        tb = pe_table.detach().to(torch.float32).contiguous()
         p = pos.to(torch.float32)
         if p.stride(-1) != 1:
             p = p.contiguous()
@@ -176,6 +174,11 @@ def nbhd_attn_fwd(q, k, v, member_idx, scale, *, bias=None, pe_idx=None, pe_tabl
 
     a.out, (a.o_sb, a.o_sh, a.o_sn) = out.data_ptr(), out.stride()[:3]
     a.lse = lse.data_ptr() if lse is not None else None
+    ws_bytes = int(lib.aff_nbhd_attn_workspace_bytes(ctypes.byref(a)))
+    if ws_bytes:
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        a.ws, a.ws_bytes = ws.data_ptr(), ws_bytes
+        keep.append(ws)
     st = lib.aff_nbhd_attn_fwd(ctypes.byref(a), _lib.stream_ptr(dev))
     _lib.check(st, "aff_nbhd_attn_fwd")
     del keep

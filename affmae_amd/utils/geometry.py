@@ -2,9 +2,13 @@
 
 ``inverse_distance_weighting`` (geometry.py:40-53) is elementwise torch
 work; ``upsample_feature_shepard`` (geometry.py:97-167) runs the HIP KNN and
-weighted-gather kernels.
+weighted-gather kernels; ``space_filling_cluster`` (geometry.py:170-319) is
+the token ordering and balanced clustering the encoder runs before every
+stage's attention blocks (aff.py:436-446), torch ops as in the reference.
 """
 from __future__ import annotations
+
+import math
 
 import torch
 
@@ -49,3 +53,97 @@ def upsample_feature_shepard(query, database, feature, database_idx=None, k=4, p
         if database_idx is not None:
             up.scatter_(dim=1, index=database_idx.long().expand(-1, -1, c), src=feature)
         return up
+
+
+def _scanline_rank(nh: int, nw: int, width: int, device) -> torch.Tensor:
+    """Rank of each cell of an nh x nw grid (row-major ids) along horizontal
+    scanlines whose direction alternates per row (geometry.py:217-229: the
+    sort key is x + y*width on even rows and (width-1) - x + y*width on odd rows)."""
+    ys, xs = torch.meshgrid(torch.arange(nh, device=device), torch.arange(nw, device=device), indexing="ij")
+    odd = (ys % 2) == 1
+    key = torch.where(odd, (width - 1) - xs, xs) + ys * width
+    order = key.reshape(-1).sort()[1]
+    rank = torch.empty_like(order)
+    rank[order] = torch.arange(order.numel(), device=device)
+    return rank, order
+
+
+def space_filling_cluster(pos, m, h, w, no_reorder=False, sf_type="", use_anchor=True):
+    """Balanced clustering along a space-filling curve (geometry.py:170-319).
+
+    pos [b,n,2] token positions (x, y) on an h x w canvas, m the cluster size.
+    With anchors (the default, used by the encoder) the canvas is cut into
+    ~n/m patches visited along alternating horizontal scanlines; a token's
+    rank is its patch's rank, ties inside a patch broken by the ratio of its
+    squared distances to the previous and next patch centres
+    (geometry.py:199-268).  Returns, like the reference,
+      no_reorder=False: (pos reordered, cluster_mean_pos [b,k,2],
+                         member_idx [b,k,m], cluster_mask [b,k,m] or None,
+                         pos_ranking [b,n,1])
+      no_reorder=True:  (cluster_mean_pos, member_idx, cluster_mask)
+    Only the scanline curve (sf_type '') is built; 'peano' and 'hilbert'
+    raise NotImplementedError.
+    """
+    if sf_type in ("peano", "hilbert"):
+        raise NotImplementedError(f"space_filling_cluster: sf_type={sf_type!r} is not built")
+    with torch.no_grad():
+        pos = pos.detach()
+        if pos.dtype != torch.float:
+            pos = pos.to(torch.float)
+        b, n, d = pos.shape
+        k = int(math.ceil(n / m))
+        dev = pos.device
+        if use_anchor:
+            patch_len = (h * w / k) ** 0.5
+            nph = int(round(h / patch_len))
+            npw = int(round(w / patch_len))
+            plh, plw = h / nph, w / npw
+            rank, order = _scanline_rank(nph, npw, w, dev)
+            ys, xs = torch.meshgrid(torch.arange(nph, device=dev), torch.arange(npw, device=dev), indexing="ij")
+            grid = torch.stack([xs, ys], dim=2).reshape(-1, 2)[order]          # cells in curve order
+            plhw = torch.tensor([plw, plh], dtype=torch.float32, device=dev)
+            centres = grid * plhw + plhw / 2 - 0.5
+            npch = centres.shape[0]
+            prev_c = torch.zeros_like(centres)
+            prev_c[1:] = centres[:npch - 1]
+            prev_c[0] = prev_c[1] - (prev_c[2] - prev_c[1])
+            next_c = torch.zeros_like(centres)
+            next_c[:npch - 1] = centres[1:]
+            next_c[-1] = next_c[-2] + (next_c[-2] - next_c[-3])
+            cell = (pos / plhw).floor()
+            cell = (cell[..., 0] + cell[..., 1] * npw).long()                  # row-major patch id
+            prank = rank.unsqueeze(0).expand(b, -1).gather(1, cell)             # b x n
+            d_prev = (pos - prev_c[prank]).pow(2).sum(-1)
+            d_next = (pos - next_c[prank]).pow(2).sum(-1)
+            ratio = d_prev / (d_next + 1e-5)
+            key = prank.unsqueeze(2) * (ratio.max() + 1) + ratio.unsqueeze(2)
+            pos_ranking = key.sort(dim=1)[1]                                     # b x n x 1
+        else:
+            rank, _ = _scanline_rank(h, w, w, dev)
+            pid = (pos[..., 0] + pos[..., 1] * w).long().reshape(-1)
+            pos_ranking = rank.gather(0, pid).reshape(b, n).sort()[1].unsqueeze(2)
+
+        pos = pos.gather(1, pos_ranking.expand(-1, -1, d))
+        if k * m == n:
+            cluster_mask = None
+            cluster_mean_pos = pos.reshape(b, k, m, d).mean(2)
+        else:
+            pos_pad = torch.zeros(b, k * m, d, dtype=pos.dtype, device=dev)
+            pos_pad[:, :n] = pos
+            cluster_mask = torch.zeros(b, k * m, device=dev).long()
+            cluster_mask[:, :n] = 1
+            cluster_mask = cluster_mask.reshape(b, k, m)
+            cluster_mean_pos = pos_pad.reshape(b, k, m, d).sum(2) / cluster_mask.sum(2, keepdim=True)
+
+        if no_reorder:
+            if k * m == n:
+                member_idx = pos_ranking.reshape(b, k, m)
+            else:
+                member_idx = torch.zeros(b, k * m, device=dev, dtype=torch.int64)
+                member_idx[:, :n] = pos_ranking.squeeze(2)
+                member_idx = member_idx.reshape(b, k, m)
+            return cluster_mean_pos, member_idx, cluster_mask
+        member_idx = torch.arange(k * m, device=dev)
+        member_idx[n:] = 0
+        member_idx = member_idx.unsqueeze(0).expand(b, -1).reshape(b, k, m)
+        return pos, cluster_mean_pos, member_idx, cluster_mask, pos_ranking

@@ -22,27 +22,37 @@ def cfg1_coords(B: int = 2, N: int = 1024, seed: int = 0) -> torch.Tensor:
     return torch.rand((B, N, 2), generator=_gen(seed), dtype=torch.float32)
 
 
-def jittered_grid(B: int, side: int, keep: int, seed: int = 0) -> torch.Tensor:
+def jittered_grid(B: int, side: int, keep: int, seed: int = 0, order: str = "sfc") -> torch.Tensor:
     """Config 2 coordinates: keep `keep` of side*side cells per image (chosen
     without replacement), each at (col, row) + U(-0.5, 0.5).
 
-    Tokens are listed in raster order of their cells, the spatially coherent
-    order in which the encoder presents tokens after its scanline clustering.
-    Returns fp32 [B, keep, 2] in grid units.
+    order "sfc" (default) lists the tokens the way the encoder hands them to
+    its attention blocks: ordered by space_filling_cluster on the cells' grid
+    positions with cluster size 8 (reference aff.py:436-446 reorders feat and
+    pos by that ranking before the blocks run).  order "raster" lists them in
+    row-major cell order.  Returns fp32 [B, keep, 2] in grid units.
     """
+    from .utils.geometry import space_filling_cluster
+
     g = _gen(seed)
     out = torch.empty((B, keep, 2), dtype=torch.float32)
     for b in range(B):
         cells = torch.randperm(side * side, generator=g)[:keep].sort().values
         row = (cells // side).to(torch.float32)
         col = (cells % side).to(torch.float32)
+        if order == "sfc":
+            cxy = torch.stack([col, row], -1).unsqueeze(0)
+            rank = space_filling_cluster(cxy, 8, side, side)[4][0, :, 0]
+            col, row = col[rank], row[rank]
+        elif order != "raster":
+            raise ValueError(f"unknown token order {order!r}")
         jit = torch.rand((keep, 2), generator=g, dtype=torch.float32) - 0.5
         out[b, :, 0] = col + jit[:, 0]
         out[b, :, 1] = row + jit[:, 1]
     return out
 
 
-def cfg2(B: int = 32, N: int = 6272, H: int = 4, D: int = 32, dtype=torch.bfloat16):
+def cfg2(B: int = 32, N: int = 6272, H: int = 4, D: int = 32, dtype=torch.bfloat16, order: str = "sfc"):
     """Config 2: neighbourhood attention at the stage-1 shape of a 448^2 image,
     patch 4, 50% mask (112 x 112 grid, 6272 visible tokens).
 
@@ -51,7 +61,7 @@ def cfg2(B: int = 32, N: int = 6272, H: int = 4, D: int = 32, dtype=torch.bfloat
     (a seeded Linear(5, H) initialisation).
     """
     side = 112
-    pos = jittered_grid(B, side, N, seed=0)
+    pos = jittered_grid(B, side, N, seed=0, order=order)
     g = _gen(1)
     q = torch.randn((B, H, N, D), generator=g).to(dtype)
     k = torch.randn((B, H, N, D), generator=g).to(dtype)

@@ -124,8 +124,14 @@ typedef struct aff_nbhd_attn_args {
     const void *blank_v;
     void *out; int64_t o_sb, o_sh, o_sn;
     float *lse;
+    void *ws; size_t ws_bytes; /* workspace: aff_nbhd_attn_workspace_bytes(args) bytes */
 } aff_nbhd_attn_args;
 
+/* Workspace the call with these arguments needs (0 when none): one byte per
+ * 16-query tile when the matrix-core path runs (16-bit q/k/v, D == 32,
+ * M <= 64, fp32 table in bias modes 2 and 4).  Its contents on entry do not
+ * matter; calls that share it must not overlap. */
+size_t aff_nbhd_attn_workspace_bytes(const aff_nbhd_attn_args *args);
 aff_status aff_nbhd_attn_fwd(const aff_nbhd_attn_args *args, aff_stream_t stream);
 
 /* ------------------------------------------------------------------------ *
