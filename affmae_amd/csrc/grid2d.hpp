@@ -85,10 +85,28 @@ inline WsLayout ws_layout(int B, const Segs &s) {
     return w;
 }
 
+// Queries per cell tile of the KNN query sort (see QueryBin), and points per
+// build thread kept in registers.
+constexpr int TILE_QUERIES = 48;
+constexpr int PPT = 8;
+
+// Optional query sort done by the build of a single-segment grid: query
+// (b, i) at q[b * q_sb + i * q_sm + {0, 1}], i < M, is written to
+// out[b * M + slot] = (x, y, i bits, 0), ordered by the cell tile of the
+// grid it falls in.  out == nullptr skips the sort.
+struct QueryBin {
+    const float *q;
+    int64_t q_sb, q_sm;
+    int M;
+    float4 *out;
+};
+
 // Builds the grids of all B * s.L segments (defined in knn.hip).
 // src: point (b, row) at src[b * sb + row * sn + {0, 1}], rows as in s.start.
 aff_status launch_build(const float *src, int64_t sb, int64_t sn, int B, const Segs &s, void *ws,
                         hipStream_t stream);
+aff_status launch_build(const float *src, int64_t sb, int64_t sn, int B, const Segs &s, void *ws,
+                        hipStream_t stream, const QueryBin &qb);
 
 // Cell coordinate of v along one axis.  Monotone non-decreasing in v, which
 // is what makes "all points with coordinate in [a, b] lie in cells
@@ -158,25 +176,30 @@ __device__ __forceinline__ void visit_disk(const SegView &g, float qx, float qy,
     }
 }
 
+// Ascending sort in registers: Batcher's odd-even merge sort network (543
+// compare-exchanges for 64 keys, against 672 for a bitonic network).  All
+// loop bounds are compile-time constants, so every index is a register.
+// Scheduling barriers every 16 compare-exchanges keep the compiler from
+// interleaving a whole stage, which would hold old and new copies of every
+// key at once.
 template <int N>
-__device__ __forceinline__ void bitonic_sort(uint64_t (&a)[N]) {
+__device__ __forceinline__ void sort_keys(uint64_t (&a)[N]) {
+    int n = 0;
 #pragma unroll
-    for (int k = 2; k <= N; k <<= 1) {
+    for (int p = 1; p < N; p <<= 1)
 #pragma unroll
-        for (int j = k >> 1; j > 0; j >>= 1) {
+        for (int k = p; k >= 1; k >>= 1)
 #pragma unroll
-            for (int i = 0; i < N; ++i) {
-                const int l = i ^ j;
-                if (l > i) {
-                    const uint64_t x = a[i], y = a[l];
-                    const bool up = (i & k) == 0;
-                    const bool sw = up ? (x > y) : (x < y);
-                    a[i] = sw ? y : x;
-                    a[l] = sw ? x : y;
-                }
-            }
-        }
-    }
+            for (int j = k % p; j + k < N; j += 2 * k)
+#pragma unroll
+                for (int i = 0; i < k && i < N - j - k; ++i)
+                    if ((i + j) / (2 * p) == (i + j + k) / (2 * p)) {
+                        const uint64_t x = a[i + j], y = a[i + j + k];
+                        const bool sw = x > y;
+                        a[i + j] = sw ? y : x;
+                        a[i + j + k] = sw ? x : y;
+                        if (N > 16 && (++n & 15) == 0) __builtin_amdgcn_sched_barrier(0);
+                    }
 }
 
 __device__ __forceinline__ float query_slack(const GridParams &p, float qx, float qy) {
@@ -200,7 +223,21 @@ __device__ __forceinline__ float initial_radius2(const SegView &g, float qx, flo
     const float gw = float(p.gx) * p.h, gh = float(p.gy) * p.h;
     const float ex = fmaxf(0.f, fmaxf(p.x0 - qx, qx - (p.x0 + gw)));
     const float ey = fmaxf(0.f, fmaxf(p.y0 - qy, qy - (p.y0 + gh)));
-    const float rad = sqrtf(target / (3.14159265f * rho)) + sqrtf(ex * ex + ey * ey);
+    float rad = sqrtf(target / (3.14159265f * rho));
+    // Near the grid's edges part of the disk holds no points: widen the
+    // radius by the inverse of the covered fraction of the disk's bounding
+    // square (twice, as the fraction shrinks with the new radius).
+    if (ex == 0.f && ey == 0.f) {
+        const float r0 = rad;
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+            const float fx = (fminf(qx + rad, p.x0 + gw) - fmaxf(qx - rad, p.x0)) / (2.f * rad);
+            const float fy = (fminf(qy + rad, p.y0 + gh) - fmaxf(qy - rad, p.y0)) / (2.f * rad);
+            const float f = fmaxf(fx * fy, 0.0625f);
+            rad = r0 * sqrtf(1.f / f);
+        }
+    }
+    rad += sqrtf(ex * ex + ey * ey);
     float U = fmaxf(rad * rad, 1e-30f);
     return U < INFINITY ? U : INFINITY;
 }
@@ -239,7 +276,7 @@ __device__ __forceinline__ void knn_select(const SegView &g, float qx, float qy,
     if (ok) {
 #pragma unroll
         for (int s = 0; s < CAP; ++s) a[s] = (s < cnt) ? col[s * stride] : ~0ull;
-        bitonic_sort<CAP>(a);
+        sort_keys<CAP>(a);
 #pragma unroll
         for (int s = 0; s < CAP; ++s)
             if (s >= k) a[s] = ~0ull;
