@@ -17,6 +17,19 @@ aff_status fail(aff_status code, const char *fmt, ...) {
 
 void clear_error() { g_last_error[0] = '\0'; }
 
+int device_cu_count() {
+    constexpr int MAXDEV = 64;
+    static int cache[MAXDEV];  // 0 = not queried yet; benign race: every writer stores the same value
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAXDEV) return 256;
+    if (cache[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cache[dev] = n;
+    }
+    return cache[dev];
+}
+
 }  // namespace aff
 
 extern "C" const char *aff_last_error(void) { return aff::g_last_error; }

@@ -20,6 +20,9 @@ void clear_error();
         if (!(cond)) return ::aff::fail(AFF_ERR_INVALID_ARG, __VA_ARGS__); \
     } while (0)
 
+// Compute units of the current device (cached per device id; 0 -> 256).
+int device_cu_count();
+
 inline aff_status check_launch(const char *what) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)

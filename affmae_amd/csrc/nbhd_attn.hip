@@ -9,21 +9,23 @@
 // Two kernels implement it.
 //
 // nbhd_attn_tile_kernel (bf16 / fp16, head_dim 32, M <= 64): one workgroup
-// takes 16 consecutive queries of one image and every head.  The tile's
-// neighbour indices are deduplicated into a "union" of at most 256 token
+// takes 32 consecutive queries of one image and every head.  The tile's
+// neighbour indices are deduplicated into a "union" of at most 224 token
 // rows (an LDS bitmap over the tile's index window plus a popcount prefix
 // gives every (query, neighbour) pair a union slot).  Per head the union's
 // K rows feed S^T = K_u Q^T on v_mfma_f32_16x16x32 (K straight from HBM/L2
 // into the A operand, Q as the B operand), S goes to LDS, the softmax runs
-// in (query, neighbour) layout - 16 lanes per query, four entries per lane -
-// and the probabilities are scattered into a dense P[16 x U] tile, zero where
-// a query does not use a union row.  O = P V_u is a second MFMA pass with V
-// staged transposed in LDS.  Every K/V row the tile touches is read once per
-// head instead of once per (query, neighbour), and both contractions run on
-// the matrix cores.  The next head's K/V/Q/bias loads are issued as soon as
-// the current head's K/V registers are consumed (after its S MFMAs and V^T
-// stores), so their latency overlaps its softmax, PV pass and store.  A tile
-// whose union exceeds 256 rows, whose index window exceeds 8192, whose
+// in (query, neighbour) layout - 8 lanes per query, one entry per neighbour
+// and lane, logits in log2 units - and the probabilities are scattered into a
+// dense P[32 x U] tile, zero where a query does not use a union row.
+// O = P V_u is a second MFMA pass with V rows staged in LDS as they are and
+// read column-wise by gfx950's transposing LDS reads, each wave owning one
+// 16 x 16 output block.  Every K/V row the tile touches is read
+// once per head instead of once per (query, neighbour), and both contractions
+// run on the matrix cores.  The next head's K/V/Q/bias loads are issued as
+// soon as the current head's K/V registers are consumed (after its S MFMAs
+// and V^T stores), so their latency overlaps its softmax, PV pass and store.
+// A tile whose union exceeds 224 rows, whose index window exceeds 8192, whose
 // neighbour lists repeat an index within one query, or whose mask differs per
 // head is flagged in the caller's workspace (one byte per tile) and computed
 // by nbhd_attn_tile_fallback_kernel, launched right after on the same stream,
@@ -39,6 +41,8 @@
 #include "common.hpp"
 
 #include <limits.h>
+
+#include <algorithm>
 
 namespace aff {
 namespace attn {
@@ -256,28 +260,70 @@ template <> struct Mfma<f16_t> {
 };
 
 namespace tile {
-constexpr int TQ = 16;               // queries per workgroup (MFMA rows)
+constexpr int TQ = 32;               // queries per workgroup (two 16-row MFMA blocks)
 constexpr int HD = 32;               // head_dim of this kernel
-constexpr int UMAX = 256;            // union rows held in LDS
+constexpr int UMAX = 224;            // union rows held in LDS
 constexpr int WWORDS = 256;          // index-window bitmap words: windows up to 8192 indices
 constexpr int MAXM = 64;             // neighbours per query
-constexpr int RJ = MAXM / 16;        // neighbour entries per lane (16 lanes per query)
-constexpr int KBW = UMAX / 64;       // 16-row K blocks per wave
-constexpr int PCI = (UMAX * 2 + THREADS - 1) / THREADS;  // V slot-pair chunks per thread
+constexpr int LPQ = 8;               // lanes per query in the softmax
+constexpr int RJ = MAXM / LPQ;       // neighbour entries per lane: j = jl + 8 r
+constexpr int KBW = (UMAX / 16 + 3) / 4;                  // 16-slot K blocks per wave
+constexpr int PCV = (UMAX * 4 + THREADS - 1) / THREADS;  // 16-byte V row pieces per thread
 constexpr int SP = UMAX + 4;         // S row pitch (fp32): 16-byte rows, 4-bank shift per row
-constexpr int PP = UMAX + 8;         // P row pitch (16-bit): 16-byte rows, column UMAX is a dummy
-constexpr int VP = UMAX + 4;         // V^T row pitch (16-bit): 8-byte rows, conflict-free pair stores
+constexpr int PP = 2 * SP;           // P row pitch (16-bit): P row q overwrites S row q in place;
+                                     // column UMAX (inside the row) is a dummy
+constexpr int VRP = 40;              // V row pitch (16-bit): 80-byte rows
+constexpr int OP = HD + 4;           // O row pitch (fp32)
+constexpr float LOG2E = 1.4426950408889634f;
 static_assert(WWORDS == THREADS, "one bitmap word per thread");
-static_assert(UMAX % 32 == 0 && (VP / 2) % 8 == 2, "V^T pitch keeps the pair stores conflict-free");
+static_assert(TQ * LPQ == THREADS, "one softmax lane group per query");
+static_assert(UMAX % 32 == 0, "union rows come in 32-row MFMA chunks");
 }  // namespace tile
 
 __device__ __forceinline__ uint4 ld16(const char *p) { return *reinterpret_cast<const uint4 *>(p); }
-__device__ __forceinline__ uint32_t ld4(const char *p) { return *reinterpret_cast<const uint32_t *>(p); }
+__device__ __forceinline__ uint2 ld8(const char *p) { return *reinterpret_cast<const uint2 *>(p); }
 
-// One workgroup per 16-query tile.  flags[tile] = 0 when the tile ran here,
-// 1 when its union does not fit (the fallback kernel then computes it).
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane 4a + b receives
+// element b of the four 16-bit values addressed by lanes a, 4 + a, 8 + a and
+// 12 + a (in that order).  With lane 4k + a pointing at row s_k, columns
+// 4a .. 4a + 3 of a row-major 16-bit tile, lane n therefore holds column n of
+// rows s_0 .. s_3: a column of the tile, as an MFMA operand wants it.
+typedef short tr_v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) tr_v4s lds_tr_v4s;
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t *p) {
+    const tr_v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_tr_v4s *)(p));
+    return __builtin_bit_cast(uint2, v);
+}
+
+// Max / sum over each aligned group of 8 lanes: two quad butterflies, then
+// the half-row mirror (lane i <-> 7 - i) folds the other quad in.
+__device__ __forceinline__ float grp8_max(float v) {
+    v = fmaxf(v, dpp_mov<0xB1>(v));
+    v = fmaxf(v, dpp_mov<0x4E>(v));
+    return fmaxf(v, dpp_mov<0x141>(v));
+}
+__device__ __forceinline__ float grp8_sum(float v) {
+    v += dpp_mov<0xB1>(v);
+    v += dpp_mov<0x4E>(v);
+    return v + dpp_mov<0x141>(v);
+}
+
+// One workgroup (4 waves) per 32-query tile of one image, every head.
+// flags[tile] = 0 when the tile ran here, 1 when it must take the per-row
+// fallback (union wider than UMAX rows, index window wider than 8192, an index
+// repeated within one query's list, or a per-head mask).
+//
+// Per head:  S^T = K_u Q^T on v_mfma_f32_16x16x32 (wave w: 16-slot blocks
+// w, w + 4, ...; both query halves share the K operand), S -> LDS; softmax
+// with 8 lanes x RJ entries per query reading S at the entries' union slots,
+// logits pre-scaled by log2(e) so one v_exp_f32 per entry; P (16-bit) to a
+// dense [query][slot] tile written over the query's own S row (non-member
+// slots 0); O = P V_u with V rows in
+// LDS, wave w owning output block (query half w & 1, channel half w >> 1);
+// normalise, add the blank value, store.  The next head's Q/K/V/bias loads
+// are issued once this head's K/V registers are consumed.
 template <typename T, int BIAS>
-__global__ __launch_bounds__(THREADS) void nbhd_attn_tile_kernel(const aff_nbhd_attn_args a) {
+__global__ __launch_bounds__(THREADS) void nbhd_attn_tile_kernel(const aff_nbhd_attn_args a, int ntiles) {
     using namespace tile;
     using MM = Mfma<T>;
     struct SetupLds {
@@ -286,36 +332,46 @@ __global__ __launch_bounds__(THREADS) void nbhd_attn_tile_kernel(const aff_nbhd_
     };
     __shared__ __align__(16) union {
         SetupLds s;
-        float S[TQ * SP];
+        float S[TQ * SP];        // scores, then (per row, in place) the 16-bit probabilities
+        uint16_t P[TQ * PP];
     } sh;
-    __shared__ __align__(16) uint16_t Pb[TQ * PP];
-    __shared__ __align__(16) uint16_t VT[HD * VP];
-    __shared__ __align__(16) float Ob[2][TQ][HD];
-    __shared__ int ulist[UMAX];
-    __shared__ uint32_t qbits[TQ][UMAX / 32];
+    uint16_t *const Pb = sh.P;
+    __shared__ __align__(16) uint16_t Vs[UMAX * VRP];
+    // the union list and the per-query slot bits are only used while setting
+    // up the tile, O only in the head loop: they share one region
+    struct UnionLds {
+        int ulist[UMAX];
+        uint32_t qbits[TQ][UMAX / 32];
+    };
+    __shared__ __align__(16) union {
+        UnionLds u;
+        float Ob[TQ * OP];
+    } sh2;
+    int *const ulist = sh2.u.ulist;
+    auto &qbits = sh2.u.qbits;
+    float *const Ob = sh2.Ob;
     __shared__ float linfo[TQ][2];
     __shared__ int red[4];
 
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    const int q = t >> 4, jl = t & 15;
+    const int q = t >> 3, jl = t & 7;  // softmax role: query q, entries jl + 8 r
     const int N = a.N, M = a.M, H = a.H;
     const int tiles = (N + TQ - 1) / TQ;
-    const uint32_t bid = xcd_swizzle(blockIdx.x, gridDim.x);
-    const int b = int(bid / tiles);
-    const int n0 = int(bid % tiles) * TQ;
+    const int rowq = lane & 15, grp = lane >> 4;
+    uint8_t *flags = static_cast<uint8_t *>(a.ws);
+    const int tile = int(xcd_swizzle(blockIdx.x, gridDim.x));
+    const int b = tile / tiles;
+    const int n0 = (tile % tiles) * TQ;
     const int n = n0 + q;
     const bool qlive = n < N;
     const int nc = min(n, N - 1);
-    const int rowq = lane & 15, grp = lane >> 4;
 
     if (t < 4) red[t] = 0;
     sh.s.bits[t] = 0;
-    if (t < TQ * UMAX / 32) (&qbits[0][0])[t] = 0;
-    for (int i = t; i < TQ * PP / 2; i += THREADS) reinterpret_cast<uint32_t *>(Pb)[i] = 0;
+    for (int i = t; i < TQ * UMAX / 32; i += THREADS) (&qbits[0][0])[i] = 0;
 
-    // ---- this lane's (query, neighbour) entries: j = jl + 16 r.  With a mask,
-    // the head-0 row is every head's row (a per-head mask sends the tile to the
-    // fallback kernel).
+    // ---- this lane's (query, neighbour) entries.  With a mask, the head-0 row
+    // is every head's row (a per-head mask sends the tile to the fallback).
     const int64_t mi_row = (int64_t)b * a.mi_sb + (int64_t)nc * a.mi_sn;
     const int64_t mk_row = (int64_t)b * a.mask_sb + (int64_t)nc * a.mask_sn;
     int idx[RJ];
@@ -323,7 +379,7 @@ __global__ __launch_bounds__(THREADS) void nbhd_attn_tile_kernel(const aff_nbhd_
     int nmask = 0;
 #pragma unroll
     for (int r = 0; r < RJ; ++r) {
-        const int j = jl + 16 * r;
+        const int j = jl + LPQ * r;
         const bool live = qlive && j < M;
         const int64_t ix = live ? load_index(a.member_idx, a.idx_is_i64, mi_row + j) : -1;
         bool ok = live && ix >= 0 && ix < N;
@@ -332,43 +388,35 @@ __global__ __launch_bounds__(THREADS) void nbhd_attn_tile_kernel(const aff_nbhd_
         idx[r] = ok ? int(ix) : 0;
         nmask += (live && !ok) ? 1 : 0;
     }
-    // coordinate terms of the bias, shared by every head (modes 3 and 4)
-    float fx[RJ], fy[RJ];
-    int tab[RJ];
+    // coordinate terms of the bias, shared by every head (modes 2-4): issued
+    // here, consumed after the union is built, so they overlap its LDS work
+    float gx_[RJ], gy_[RJ];
+    int64_t gpe[RJ];
+    float pqx = 0.f, pqy = 0.f;
 #pragma unroll
     for (int r = 0; r < RJ; ++r) {
-        fx[r] = fy[r] = 0.f;
-        tab[r] = -1;
+        gx_[r] = gy_[r] = 0.f;
+        gpe[r] = -1;
     }
     if constexpr (BIAS == 2) {
 #pragma unroll
         for (int r = 0; r < RJ; ++r)
-            if (use[r]) {
-                const int64_t v =
-                    load_index(a.pe_idx, a.pe_is_i64, (int64_t)b * a.pe_sb + (int64_t)nc * a.pe_sn + jl + 16 * r);
-                tab[r] = (v >= 0 && v < a.table_rows) ? int(v) : -1;
-            }
+            if (use[r])
+                gpe[r] = load_index(a.pe_idx, a.pe_is_i64, (int64_t)b * a.pe_sb + (int64_t)nc * a.pe_sn + jl + LPQ * r);
     } else if constexpr (BIAS == 3 || BIAS == 4) {
         const float *pos_b = a.pos + (int64_t)b * a.pos_sb;
-        const float pqx = pos_b[(int64_t)nc * a.pos_sn], pqy = pos_b[(int64_t)nc * a.pos_sn + 1];
-        const float relW = float(a.rel_width), relT = float(2 * a.rel_width + 1);
+        pqx = pos_b[(int64_t)nc * a.pos_sn];
+        pqy = pos_b[(int64_t)nc * a.pos_sn + 1];
 #pragma unroll
         for (int r = 0; r < RJ; ++r)
             if (use[r]) {
-                const float mx = pos_b[(int64_t)idx[r] * a.pos_sn], my = pos_b[(int64_t)idx[r] * a.pos_sn + 1];
-                if constexpr (BIAS == 4) {
-                    const int64_t v = pe_from_coords(pqx, pqy, mx, my, relW, relT);
-                    tab[r] = (v >= 0 && v < a.table_rows) ? int(v) : -1;
-                } else {
-                    fx[r] = mx - pqx;
-                    fy[r] = my - pqy;
-                }
+                gx_[r] = pos_b[(int64_t)idx[r] * a.pos_sn];
+                gy_[r] = pos_b[(int64_t)idx[r] * a.pos_sn + 1];
             }
     }
 
     // ---- union of the tile's neighbour rows over the index window
-    // [wlo, wlo + 8192) around the tile (every index when N <= 8192); an index
-    // outside it, or a mask that differs per head, flags the tile
+    // [wlo, wlo + 8192) around the tile (every index when N <= 8192)
     const int wlo = max(0, min(n0 + TQ / 2 - WWORDS * 16, N - WWORDS * 32));
     bool outside = false;
 #pragma unroll
@@ -379,10 +427,9 @@ __global__ __launch_bounds__(THREADS) void nbhd_attn_tile_kernel(const aff_nbhd_
             else outside = true;
         }
     if (outside) red[0] = 1;
-    uint8_t *flags = static_cast<uint8_t *>(a.ws);
     lds_barrier();
     if ((a.mask && a.mask_sh != 0) || red[0]) {
-        if (t == 0) flags[bid] = 1;
+        if (t == 0) flags[tile] = 1;
         return;
     }
     if (w == 0) {
@@ -410,7 +457,7 @@ __global__ __launch_bounds__(THREADS) void nbhd_attn_tile_kernel(const aff_nbhd_
     lds_barrier();
     const int U = red[2];
     if (U > UMAX) {
-        if (t == 0) flags[bid] = 1;
+        if (t == 0) flags[tile] = 1;
         return;
     }
     int slot[RJ];
@@ -428,21 +475,41 @@ __global__ __launch_bounds__(THREADS) void nbhd_attn_tile_kernel(const aff_nbhd_
     }
     lds_barrier();
     if (red[3]) {
-        if (t == 0) flags[bid] = 1;
+        if (t == 0) flags[tile] = 1;
         return;
     }
-    if (t == 0) flags[bid] = 0;
+    if (t == 0) flags[tile] = 0;
+
+    // bias terms from the gathered coordinates / pe indices
+    float fx[RJ], fy[RJ];
+    int tab[RJ];
+#pragma unroll
+    for (int r = 0; r < RJ; ++r) {
+        fx[r] = fy[r] = 0.f;
+        tab[r] = -1;
+        if constexpr (BIAS == 2) {
+            if (use[r]) tab[r] = (gpe[r] >= 0 && gpe[r] < a.table_rows) ? int(gpe[r]) : -1;
+        } else if constexpr (BIAS == 4) {
+            if (use[r]) {
+                const int64_t v = pe_from_coords(pqx, pqy, gx_[r], gy_[r], float(a.rel_width),
+                                                 float(2 * a.rel_width + 1));
+                tab[r] = (v >= 0 && v < a.table_rows) ? int(v) : -1;
+            }
+        } else if constexpr (BIAS == 3) {
+            fx[r] = gx_[r] - pqx;
+            fy[r] = gy_[r] - pqy;
+        }
+    }
 
     const int Up = (U + 31) & ~31;
     const int nkb = Up >> 4, nkb2 = Up >> 5;
     const bool blank = a.blank_k != nullptr;
-    const float scale = a.scale;
-    const int nm = nmask;
+    const float scale2 = a.scale * LOG2E;
+    const float nmq = grp8_sum(float(nmask));  // masked (live) entries of this query
 
     // ---- per-lane byte offsets into one head's planes, the same for every head
     // (the host guarantees they fit in 32 bits).  Union slots past U read the
-    // first union row: their S columns are never read and their P columns stay
-    // zero.  Unused entries read S and write P in the dummy column UMAX.
+    // first union row for K (their S columns are never read) and zero for V.
     const int row0 = U > 0 ? ulist[0] : 0;
     const uint32_t ksn2 = uint32_t(a.k_sn * 2), vsn2 = uint32_t(a.v_sn * 2);  // < 2^24, host-checked
     uint32_t koff[KBW];
@@ -451,21 +518,26 @@ __global__ __launch_bounds__(THREADS) void nbhd_attn_tile_kernel(const aff_nbhd_
         const int s = (w + 4 * i) * 16 + rowq;
         koff[i] = __umul24(uint32_t(s < U ? ulist[s] : row0), ksn2) + grp * 16;
     }
-    uint32_t voff[PCI][2];
+    // V row pieces: piece pc = t + 256 i is row pc >> 2, channels 8 (pc & 3) .. +8
+    uint32_t voff[PCV];
 #pragma unroll
-    for (int i = 0; i < PCI; ++i) {
-        const int pc = t + THREADS * i, s = 2 * (pc >> 2), dc = pc & 3;
-        voff[i][0] = __umul24(uint32_t(s < U ? ulist[s] : row0), vsn2) + dc * 16;
-        voff[i][1] = __umul24(uint32_t(s + 1 < U ? ulist[s + 1] : row0), vsn2) + dc * 16;
+    for (int i = 0; i < PCV; ++i) {
+        const int pc = t + THREADS * i, s = pc >> 2, dc = pc & 3;
+        voff[i] = __umul24(uint32_t(s < U ? ulist[s] : row0), vsn2) + dc * 16;
     }
-    const uint32_t qoff = uint32_t(((int64_t)min(n0 + rowq, N - 1) * a.q_sn + grp * 8) * 2);
-    const uint32_t qpoff = uint32_t(((int64_t)nc * a.q_sn + 2 * jl) * 2);
-    int sidx[RJ], pidx[RJ];
+    // softmax entries: LDS byte offsets of S[q][slot] and P[q][slot]
+    uint32_t sadr[RJ], padr[RJ];
 #pragma unroll
     for (int r = 0; r < RJ; ++r) {
-        sidx[r] = q * SP + slot[r];
-        pidx[r] = q * PP + slot[r];
+        sadr[r] = uint32_t((q * SP + slot[r]) * 4);
+        padr[r] = uint32_t((q * PP + slot[r]) * 2);
     }
+    const int trk = (lane & 15) >> 2, tra = lane & 3;  // transposing-read role: row k, columns 4a
+    uint32_t qoff[2];
+#pragma unroll
+    for (int qh = 0; qh < 2; ++qh)
+        qoff[qh] = uint32_t(((int64_t)min(n0 + 16 * qh + rowq, N - 1) * a.q_sn + grp * 8) * 2);
+    const uint32_t qboff = uint32_t(((int64_t)nc * a.q_sn + 4 * jl) * 2);  // blank logit: channels 4 jl .. +4
     const float *table = static_cast<const float *>(a.table);
     const int64_t brow = (int64_t)b * a.bias_sb + (int64_t)nc * a.bias_sn;
     const char *qb = static_cast<const char *>(a.q) + (int64_t)b * a.q_sb * 2;
@@ -474,36 +546,34 @@ __global__ __launch_bounds__(THREADS) void nbhd_attn_tile_kernel(const aff_nbhd_
     const int64_t qsh = a.q_sh * 2, ksh = a.k_sh * 2, vsh = a.v_sh * 2;
 
     // ---- registers of one head, loaded one head ahead
-    uint4 qf, kf[KBW], vr[PCI][2];
-    uint32_t qpair = 0, bkpair = 0, bvpair = 0;
+    uint4 qf[2], kf[KBW], vr[PCV];
+    uint2 qb4 = make_uint2(0, 0), bk4 = make_uint2(0, 0), bv4 = make_uint2(0, 0);
     float bs[RJ];
     auto load_head = [&](int h) {
         const char *Qh = qb + h * qsh, *Kh = kb_ + h * ksh, *Vh = vb + h * vsh;
-        qf = ld16(Qh + qoff);  // B operand of S^T = K_u Q^T: query rowq, channels 8*grp .. +8
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh) qf[qh] = ld16(Qh + qoff[qh]);  // B operand: query rows, 8 channels
         if (blank) {
-            qpair = ld4(Qh + qpoff);
-            bkpair = ld4(static_cast<const char *>(a.blank_k) + (h * HD + 2 * jl) * 2);
-            bvpair = ld4(static_cast<const char *>(a.blank_v) + (h * HD + 2 * jl) * 2);
+            qb4 = ld8(Qh + qboff);
+            bk4 = ld8(static_cast<const char *>(a.blank_k) + (h * HD + 4 * jl) * 2);
+            bv4 = ld8(static_cast<const char *>(a.blank_v) + (h * HD + 4 * jl) * 2);
         }
 #pragma unroll
         for (int i = 0; i < KBW; ++i)
-            if (w + 4 * i < nkb) kf[i] = ld16(Kh + koff[i]);  // A operand: union row, channels 8*grp .. +8
+            if (w + 4 * i < nkb) kf[i] = ld16(Kh + koff[i]);  // A operand: union row, 8 channels
 #pragma unroll
-        for (int i = 0; i < PCI; ++i)
-            if (32 * w + 128 * i < Up) {  // this wave's slot range [32w + 128i, +32) is in use
-                vr[i][0] = ld16(Vh + voff[i][0]);
-                vr[i][1] = ld16(Vh + voff[i][1]);
-            }
+        for (int i = 0; i < PCV; ++i)
+            if (16 * w + 64 * i < Up) vr[i] = ld16(Vh + voff[i]);  // this wave's rows [16w + 64i, +16)
         // raw values: the selects wait until use, so these loads stay in flight
 #pragma unroll
         for (int r = 0; r < RJ; ++r) {
             if constexpr (BIAS == 1) {
-                bs[r] = load_any(a.bias, a.bias_dtype, brow + (int64_t)h * a.bias_sh + jl + 16 * r);
+                bs[r] = use[r] ? load_any(a.bias, a.bias_dtype, brow + (int64_t)h * a.bias_sh + jl + LPQ * r) : 0.f;
             } else if constexpr (BIAS == 2 || BIAS == 4) {
-                bs[r] = table[(tab[r] >= 0 ? tab[r] : 0) * H + h];
+                bs[r] = tab[r] >= 0 ? table[tab[r] * H + h] : 0.f;
             } else if constexpr (BIAS == 3) {
                 const float *pw = a.pos_w + h * 5;
-                bs[r] = cont_bias(pw, a.pos_b[h], fx[r], fy[r]);
+                bs[r] = use[r] ? cont_bias(pw, a.pos_b[h], fx[r], fy[r]) : 0.f;
             } else {
                 bs[r] = 0.f;
             }
@@ -512,112 +582,125 @@ __global__ __launch_bounds__(THREADS) void nbhd_attn_tile_kernel(const aff_nbhd_
 
     load_head(0);
     for (int h = 0; h < H; ++h) {
-        // V^T from the prefetched slot pairs: one 32-bit store per channel
+        // V rows into LDS as they are (rows past U as zeros): one 16-byte store per piece
 #pragma unroll
-        for (int i = 0; i < PCI; ++i)
-            if (32 * w + 128 * i < Up) {
-                const int pc = t + THREADS * i, s = 2 * (pc >> 2), dc = pc & 3;
-                const uint32_t x[4] = {vr[i][0].x, vr[i][0].y, vr[i][0].z, vr[i][0].w};
-                const uint32_t y[4] = {vr[i][1].x, vr[i][1].y, vr[i][1].z, vr[i][1].w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    *reinterpret_cast<uint32_t *>(&VT[(dc * 8 + 2 * e) * VP + s]) =
-                        __builtin_amdgcn_perm(y[e], x[e], 0x05040100u);
-                    *reinterpret_cast<uint32_t *>(&VT[(dc * 8 + 2 * e + 1) * VP + s]) =
-                        __builtin_amdgcn_perm(y[e], x[e], 0x07060302u);
-                }
+        for (int i = 0; i < PCV; ++i)
+            if (16 * w + 64 * i < Up) {
+                const int pc = t + THREADS * i, s = pc >> 2, dc = pc & 3;
+                *reinterpret_cast<uint4 *>(&Vs[s * VRP + dc * 8]) = s < U ? vr[i] : make_uint4(0, 0, 0, 0);
             }
-        // S^T blocks -> S[query][slot]
+        // S^T blocks (16 slots x 16 queries) -> S[query][slot]
 #pragma unroll
         for (int i = 0; i < KBW; ++i)
             if (w + 4 * i < nkb) {
                 const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-                const f32x4 sv = MM::mma(kf[i], qf, z);
-                *reinterpret_cast<f32x4 *>(&sh.S[rowq * SP + (w + 4 * i) * 16 + 4 * grp]) = sv;
+#pragma unroll
+                for (int qh = 0; qh < 2; ++qh) {
+                    const f32x4 sv = MM::mma(kf[i], qf[qh], z);
+                    *reinterpret_cast<f32x4 *>(&sh.S[(16 * qh + rowq) * SP + (w + 4 * i) * 16 + 4 * grp]) = sv;
+                }
             }
-        const uint32_t qp = qpair, bkp = bkpair, bvp = bvpair;
+        const uint2 qp = qb4, bkp = bk4, bvp = bv4;
         float bcur[RJ];
 #pragma unroll
-        for (int r = 0; r < RJ; ++r) bcur[r] = bs[r];  // selected at use: the entry's mask or table row
+        for (int r = 0; r < RJ; ++r) bcur[r] = bs[r];
         // this head's K/V registers are consumed: the next head's loads now have the
         // whole softmax, PV pass and store of this head to arrive
         if (h + 1 < H) load_head(h + 1);
         lds_barrier();
 
-        // ---- softmax in (query, neighbour) layout: 16 lanes per query
+        // ---- softmax in (query, neighbour) layout, log2 units
         float s_[RJ];
-        float mloc = MASKED_LOGIT;
+        float mloc = MASKED_LOGIT * LOG2E;
 #pragma unroll
         for (int r = 0; r < RJ; ++r) {
-            float bias = bcur[r];
-            if constexpr (BIAS == 2 || BIAS == 4) bias = tab[r] >= 0 ? bias : 0.f;
-            const float v = sh.S[sidx[r]] * scale + bias;
+            const float v = *reinterpret_cast<const float *>(reinterpret_cast<const char *>(sh.S) + sadr[r]) * scale2 +
+                            bcur[r] * LOG2E;
             s_[r] = use[r] ? v : -INFINITY;
             mloc = fmaxf(mloc, s_[r]);
         }
         float sb = 0.f;
         if (blank) {
-            const float part = MM::to_f32(uint16_t(qp & 0xffffu)) * MM::to_f32(uint16_t(bkp & 0xffffu)) +
-                               MM::to_f32(uint16_t(qp >> 16)) * MM::to_f32(uint16_t(bkp >> 16));
-            sb = row16_sum(part) * scale;
+            float part = 0.f;
+            const uint32_t qw[2] = {qp.x, qp.y}, kw[2] = {bkp.x, bkp.y};
+#pragma unroll
+            for (int e = 0; e < 2; ++e)
+                part += MM::to_f32(uint16_t(qw[e] & 0xffffu)) * MM::to_f32(uint16_t(kw[e] & 0xffffu)) +
+                        MM::to_f32(uint16_t(qw[e] >> 16)) * MM::to_f32(uint16_t(kw[e] >> 16));
+            sb = grp8_sum(part) * scale2;
             mloc = fmaxf(mloc, sb);
         }
-        const float m = row16_max(mloc);
-        float lsum = nm ? float(nm) * __expf(MASKED_LOGIT - m) : 0.f;
+        const float m = grp8_max(mloc);
+        // P row q overwrites S row q: clear the row's P span first (every union
+        // slot a query does not use must read 0).  The 8 lanes of a query are in
+        // one wave, whose LDS operations run in order, so the row's S reads above
+        // complete before these stores.
+        {
+            uint4 *prow = reinterpret_cast<uint4 *>(Pb + q * PP);
+            for (int c = jl; c < Up / 8; c += LPQ) prow[c] = make_uint4(0, 0, 0, 0);
+        }
+        float lsum = 0.f;
 #pragma unroll
         for (int r = 0; r < RJ; ++r) {
-            const float p = __expf(s_[r] - m);
-            lsum += p;
-            Pb[pidx[r]] = MM::from_f32(p);
+            const float pr = __builtin_amdgcn_exp2f(s_[r] - m);
+            lsum += pr;
+            *reinterpret_cast<uint16_t *>(reinterpret_cast<char *>(Pb) + padr[r]) = MM::from_f32(pr);
         }
-        const float pblank = blank ? __expf(sb - m) : 0.f;
-        const float l = row16_sum(lsum) + pblank;
+        const float pblank = blank ? __builtin_amdgcn_exp2f(sb - m) : 0.f;
+        const float l = grp8_sum(lsum) + pblank + (nmq > 0.f ? nmq * __builtin_amdgcn_exp2f(MASKED_LOGIT * LOG2E - m) : 0.f);
         if (jl == 0) {
             linfo[q][0] = __builtin_amdgcn_rcpf(l + 1e-12f);  // 1 ulp: outputs are 16-bit
             linfo[q][1] = pblank;
-            if (a.lse && qlive) a.lse[((int64_t)b * H + h) * N + n] = m + __logf(l + 1e-12f);
+            if (a.lse && qlive) a.lse[((int64_t)b * H + h) * N + n] = m * 0.6931471805599453f + __logf(l + 1e-12f);
         }
         lds_barrier();
 
-        // ---- O = P V_u.  Wave w: channel half (w & 1), 32-slot blocks of parity (w >> 1).
+        // ---- O = P V_u: wave w owns queries 16 (w & 1) .. +16, channels 16 (w >> 1) .. +16;
+        // the B operand (8 slots of channel 16 ch + rowq) comes from two transposing reads
         {
-            const int hd = w & 1;
+            const int qh = w & 1, ch = w >> 1;
             f32x4 o = {0.f, 0.f, 0.f, 0.f};
-            for (int kb2 = w >> 1; kb2 < nkb2; kb2 += 2) {
+            const uint16_t *vcol = Vs + (8 * grp + trk) * VRP + 16 * ch + 4 * tra;
+            for (int kb2 = 0; kb2 < nkb2; ++kb2) {
                 const int col = kb2 * 32 + 8 * grp;
-                const uint4 pa = *reinterpret_cast<const uint4 *>(&Pb[rowq * PP + col]);
-                const uint2 va = *reinterpret_cast<const uint2 *>(&VT[(rowq + 16 * hd) * VP + col]);
-                const uint2 vb2 = *reinterpret_cast<const uint2 *>(&VT[(rowq + 16 * hd) * VP + col + 4]);
+                const uint4 pa = *reinterpret_cast<const uint4 *>(&Pb[(16 * qh + rowq) * PP + col]);
+                const uint2 va = lds_read_tr16(vcol + kb2 * 32 * VRP);
+                const uint2 vb2 = lds_read_tr16(vcol + (kb2 * 32 + 4) * VRP);
                 o = MM::mma(pa, make_uint4(va.x, va.y, vb2.x, vb2.y), o);
             }
 #pragma unroll
-            for (int i = 0; i < 4; ++i) Ob[w >> 1][4 * grp + i][rowq + 16 * hd] = o[i];
+            for (int i = 0; i < 4; ++i) Ob[(16 * qh + 4 * grp + i) * OP + 16 * ch + rowq] = o[i];
         }
         lds_barrier();
 
-        // ---- two partial sums, blank value, normalise, store
+        // ---- normalise, blank value, store: query q, channels 4 jl .. +4
         {
-            const int d0 = 2 * jl;
-            const float2 p0 = *reinterpret_cast<const float2 *>(&Ob[0][q][d0]);
-            const float2 p1 = *reinterpret_cast<const float2 *>(&Ob[1][q][d0]);
+            const int d0 = 4 * jl;
+            const float4 ov = *reinterpret_cast<const float4 *>(&Ob[q * OP + d0]);
             const float pbv = linfo[q][1], inv = linfo[q][0];
-            float x0 = p0.x + p1.x, x1 = p0.y + p1.y;
+            float x[4] = {ov.x, ov.y, ov.z, ov.w};
             if (blank) {
-                x0 += pbv * MM::to_f32(uint16_t(bvp & 0xffffu));
-                x1 += pbv * MM::to_f32(uint16_t(bvp >> 16));
+                const uint32_t vw[2] = {bvp.x, bvp.y};
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    x[2 * e] += pbv * MM::to_f32(uint16_t(vw[e] & 0xffffu));
+                    x[2 * e + 1] += pbv * MM::to_f32(uint16_t(vw[e] >> 16));
+                }
             }
-            const uint32_t packed = uint32_t(MM::from_f32(x0 * inv)) | (uint32_t(MM::from_f32(x1 * inv)) << 16);
+            uint2 packed;
+            packed.x = uint32_t(MM::from_f32(x[0] * inv)) | (uint32_t(MM::from_f32(x[1] * inv)) << 16);
+            packed.y = uint32_t(MM::from_f32(x[2] * inv)) | (uint32_t(MM::from_f32(x[3] * inv)) << 16);
             if (qlive)
-                *reinterpret_cast<uint32_t *>(static_cast<T *>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh +
-                                              (int64_t)n * a.o_sn + d0) = packed;
+                *reinterpret_cast<uint2 *>(static_cast<T *>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh +
+                                           (int64_t)n * a.o_sn + d0) = packed;
         }
-        // The next head's first LDS writes (V^T, S) touch regions whose last readers
+        // The next head's first LDS writes (V, S) touch regions whose last readers
         // (PV, softmax) finished before the barrier above; its Ob / linfo writes come
         // after its own first barrier, which every lane reaches only after this store.
     }
 }
 
-// The tiles the MFMA kernel flagged: their 16 x H rows through the per-row routine.
+// The tiles the MFMA kernel flagged: their TQ x H rows through the per-row routine.
 template <typename T, int BIAS>
 __global__ __launch_bounds__(THREADS) void nbhd_attn_tile_fallback_kernel(const aff_nbhd_attn_args a, int ntiles) {
     using namespace tile;
@@ -659,8 +742,10 @@ KernelFn pick_d(int D, int mode) {
     }
 }
 
+using TileFn = void (*)(const aff_nbhd_attn_args, int);
+
 template <typename T>
-KernelFn pick_tile(int mode) {
+TileFn pick_tile(int mode) {
     switch (mode) {
         case 0: return nbhd_attn_tile_kernel<T, 0>;
         case 1: return nbhd_attn_tile_kernel<T, 1>;
@@ -759,7 +844,7 @@ extern "C" aff_status aff_nbhd_attn_fwd(const aff_nbhd_attn_args *args, aff_stre
                         (long long)ntiles, a.ws ? a.ws_bytes : (size_t)0);
         const bool bf = a.dtype == AFF_BF16;
         hipLaunchKernelGGL(bf ? attn::pick_tile<bf16_t>(a.bias_mode) : attn::pick_tile<f16_t>(a.bias_mode),
-                           dim3((unsigned)ntiles), dim3(attn::THREADS), 0, hs, a);
+                           dim3((unsigned)ntiles), dim3(attn::THREADS), 0, hs, a, (int)ntiles);
         aff_status st = check_launch("aff_nbhd_attn_fwd (tiles)");
         if (st != AFF_OK) return st;
         // flagged tiles: a grid-stride pass whose blocks skip unflagged tiles
