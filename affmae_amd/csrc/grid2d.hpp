@@ -119,12 +119,14 @@ __device__ __forceinline__ int cell_coord(float v, float origin, float inv_h, in
 }
 
 // d2 = fl(fl(dx*dx) + fl(dy*dy)): no fused multiply-add, so the value (and
-// therefore the tie order) is the one a plain fp32 CPU evaluation gives.
+// therefore the tie order) is the one a plain fp32 CPU evaluation gives.  The
+// empty asm statement hides the products from the optimiser, so neither can be
+// fused into the add, whatever contraction mode the including file uses.
 __device__ __forceinline__ float dist2(float ax, float ay, float bx, float by) {
-#pragma clang fp contract(off)
-    float dx = __fsub_rn(ax, bx);
-    float dy = __fsub_rn(ay, by);
-    return __fadd_rn(__fmul_rn(dx, dx), __fmul_rn(dy, dy));
+    const float dx = ax - bx, dy = ay - by;
+    float px = dx * dx, py = dy * dy;
+    asm volatile("" : "+v"(px), "+v"(py));
+    return px + py;
 }
 
 __device__ __forceinline__ uint64_t make_key(float d2, int idx) {
