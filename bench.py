@@ -67,6 +67,20 @@ def cfg4_bytes(w) -> int:
             + B4 * Nq * H4 * C4 * w["values"].element_size())
 
 
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (lines "traffic: <kernel> <bytes>"), or None."""
+    f = ROOT / "profiles" / "hbm_traffic_fetch_write.md"
+    try:
+        for line in f.read_text().splitlines():
+            parts = line.split()
+            if len(parts) == 3 and parts[0] == "traffic:" and parts[1] == kernel:
+                return int(parts[2])
+    except OSError:
+        pass
+    return None
+
+
 def time_events(fn, reps: int):
     """Average duration (ms) of fn() over reps, HIP events on the current stream."""
     import torch
@@ -148,6 +162,57 @@ def cpu_baseline(w, table_cpu, budget_s: float):
     }
 
 
+COPY_BYTES = 256 << 20     # size of the calibration copy of --only copy
+
+
+def only_kernel(name: str, steps: int) -> int:
+    """Launch one kernel family `steps` times on its full-size workload (inputs
+    prepared first, one launch untimed), for counter runs under rocprofv3.
+    `copy` is a plain device copy of COPY_BYTES (reads and writes COPY_BYTES):
+    the calibration of FETCH_SIZE / WRITE_SIZE."""
+    import torch
+    import torch.nn.functional as F
+    from affmae_amd import workloads
+    from affmae_amd.kernels.knn import knn_launch
+
+    dev = torch.device("cuda:0")
+    if name == "copy":
+        src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        fn = lambda: dst.copy_(src)
+    elif name in ("attn", "knn"):
+        from affmae_amd.kernels.local_attn import nbhd_attn_fwd
+        from affmae_amd.utils.pos_embed import pre_table_fp32
+        g = {n: t.to(dev) for n, t in workloads.cfg2(B=B, N=N, H=H, D=D).items()}
+        if name == "knn":
+            fn = lambda: knn_launch(g["pos"], g["pos"], K_NN, out_dtype=torch.int32)
+        else:
+            table = F.linear(pre_table_fp32.to(dev), g["pos_w"], g["pos_b"]).contiguous()
+            idx = knn_launch(g["pos"], g["pos"], K_NN, out_dtype=torch.int32)
+            out = torch.empty((B, H, N, D), dtype=torch.bfloat16, device=dev)
+            fn = lambda: nbhd_attn_fwd(g["q"], g["k"], g["v"], idx, D ** -0.5, pos=g["pos"], pe_table=table,
+                                       blank_k=g["blank_k"], blank_v=g["blank_v"], out=out, return_lse=False)
+    elif name == "merge":
+        from affmae_amd.kernels.weighted_gather import softmax_merge_launch
+        w3 = workloads.cfg3(B=32)
+        sp, mp, f = w3["src_pos"].to(dev), w3["merged_pos"].to(dev), w3["feat"].to(dev)
+        idx = knn_launch(mp, sp, 48, out_dtype=torch.int32)
+        fo = torch.empty((32, 2509, 128), dtype=torch.bfloat16, device=dev)
+        po = torch.empty((32, 2509, 2), dtype=torch.float32, device=dev)
+        fn = lambda: softmax_merge_launch(mp, sp, f, idx, 0.1, out=fo, out_pos=po)
+    elif name == "deform":
+        from affmae_amd.kernels.fused_deform_attn import ms_deformable_attention
+        w4 = workloads.cfg4(B=32)
+        g4 = {n: (v.to(dev) if torch.is_tensor(v) else v) for n, v in w4.items()}
+        fn = lambda: ms_deformable_attention(g4["query_pos"], g4["kv_pos"], g4["level_start"], g4["offsets"],
+                                             g4["attn"], g4["values"], power=3.0, k=3, weighting="idw")
+    else:
+        raise SystemExit(f"unknown --only kernel {name!r}")
+    ms = time_events(fn, steps)
+    print(json.dumps({"only": name, "launches": steps + 1, "ms_per_launch": ms}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -155,8 +220,12 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-oracle work (0 = skip)")
     ap.add_argument("--no-other", action="store_true", help="skip the config-3/4 kernel timings")
+    ap.add_argument("--only", choices=("attn", "knn", "merge", "deform", "copy"),
+                    help="launch only this kernel family --steps times (for rocprofv3 counter runs)")
     args = ap.parse_args()
 
+    if args.only and args.gpus == 1:
+        return only_kernel(args.only, args.steps)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (--gpus {args.gpus} requested). Every hot-path op is "
               "independent per image, so the batch shards across GPUs with no exchange; multi-GPU runs are "
@@ -258,7 +327,7 @@ def main() -> int:
             "peak": HBM_PEAK / 1e9,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK,
-            "traffic": None,
+            "traffic": measured_traffic("attn"),
             "algorithmic_bytes": a_bytes,
         },
         "cpu_baseline": cpu,
