@@ -66,6 +66,15 @@ __device__ __forceinline__ int64_t pe_from_coords(float qx, float qy, float mx, 
     return (int64_t)(ry * T + rx);
 }
 
+// The same in 32-bit integers: every clamped offset gives a row below T * T.
+__device__ __forceinline__ int pe_from_coords32(float qx, float qy, float mx, float my, float W, float T) {
+#pragma clang fp contract(off)
+    float rx = mx - (qx - W), ry = my - (qy - W);
+    rx = fminf(fmaxf(rx, 0.f), 2.f * W);
+    ry = fminf(fmaxf(ry, 0.f), 2.f * W);
+    return int(ry * T + rx);
+}
+
 // Continuous relative-position features f(dx, dy) = (dx, dy, r, dy/r, dx/r).
 __device__ __forceinline__ float cont_bias(const float *pw, float pb, float dx, float dy) {
     const float r = sqrtf(dx * dx + dy * dy);
@@ -415,6 +424,9 @@ __global__ __launch_bounds__(THREADS) void nbhd_attn_tile_kernel(const aff_nbhd_
             }
     }
 
+    // the cleared bitmap and counters are visible before any wave's atomics
+    lds_barrier();
+
     // ---- union of the tile's neighbour rows over the index window
     // [wlo, wlo + 8192) around the tile (every index when N <= 8192)
     const int wlo = max(0, min(n0 + TQ / 2 - WWORDS * 16, N - WWORDS * 32));
@@ -717,6 +729,479 @@ __global__ __launch_bounds__(THREADS) void nbhd_attn_tile_fallback_kernel(const 
     }
 }
 
+// ------------------------------------------------------------------------
+// Wave-per-head tile kernel (16-bit q/k/v, head_dim 32, M <= 64, bias modes
+// 0, 2 and 4).
+//
+// One workgroup takes 32 consecutive queries of one image.  Set-up (all four
+// waves) builds the union of the tile's neighbour rows as the tile kernel
+// above does, and a dense [query][union slot] table `pw` of 16-bit codes:
+// 0 = the slot is not one of the query's neighbours, 1 = neighbour with a
+// zero bias, e >= 2 = neighbour whose bias is entry e of the bias window `tw`.
+// The window holds the rows of the [T*T, H] bias table that the tile's
+// (query, neighbour) offsets select - a few hundred entries for spatially
+// coherent tokens - so every bias read is an LDS read; a tile whose offsets
+// span more than the window reads the table in global memory instead
+// (e = 2 + table row).  tw entry 0 is -inf and entry 1 is 0 for every head.
+//
+// Then each wave owns one head at a time and runs without workgroup
+// barriers.  Per 32-slot chunk of the union:
+//   S^T (32 slots x 32 queries) = K_chunk Q^T       2 x v_mfma_f32_32x32x16
+//   logits (log2 units) = S * scale * log2(e) + bias(pw) * log2(e)
+//   online softmax per query: lane l and lane l ^ 32 hold the 16 + 16 slots
+//   of query l & 31, so the chunk maximum is one permlane32 swap
+//   O^T (32 channels x 32 queries) += V_chunk^T P^T    2 x v_mfma_f32_32x32x16
+// P^T is the S result itself converted to 16 bits: the PV contraction takes
+// its k index in the order the S result lays slots out in the lanes, and
+// V^T is read in that same order from the chunk's V rows in LDS by
+// ds_read_b64_tr_b16.  K and V rows are fetched one chunk ahead.
+// Tiles this kernel cannot take (union wider than 224 rows, index window
+// wider than 8192, an index repeated within one query, a per-head mask) run
+// the per-row routine in the same workgroup.
+// ------------------------------------------------------------------------
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <typename T> struct Mfma32;
+template <> struct Mfma32<bf16_t> {
+    typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+    __device__ __forceinline__ static f32x16 mma(uint4 a, uint4 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0,
+                                                       0, 0);
+    }
+    // one v_cvt_pk_bf16_f32 (round to nearest even)
+    __device__ __forceinline__ static uint32_t pack2(float lo, float hi) {
+        typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+        typedef float f2 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, b2));
+    }
+    __device__ __forceinline__ static float to_f32(uint16_t x) { return bf16_to_f32(x); }
+};
+template <> struct Mfma32<f16_t> {
+    typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+    __device__ __forceinline__ static f32x16 mma(uint4 a, uint4 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0, 0,
+                                                      0);
+    }
+    // one v_cvt_pk_f16_f32 (round to nearest even)
+    __device__ __forceinline__ static uint32_t pack2(float lo, float hi) {
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        typedef float f2 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, h2));
+    }
+    __device__ __forceinline__ static float to_f32(uint16_t x) { return float(__builtin_bit_cast(_Float16, x)); }
+};
+
+namespace wt {
+constexpr int TQ = 32;            // queries per workgroup (the MFMA N dimension)
+constexpr int HD = 32;            // head_dim
+constexpr int UMAX = 224;         // union rows: 7 chunks of 32
+constexpr int WWORDS = 256;       // index-window bitmap words: windows up to 8192 indices
+constexpr int MAXM = 64;          // neighbours per query
+constexpr int LPQ = 8;            // set-up lanes per query
+constexpr int RJ = MAXM / LPQ;    // set-up entries per lane: j = jl + 8 r
+constexpr int NW = THREADS / 64;  // waves; wave w takes heads w, w + NW, ...
+constexpr int PWP = UMAX + 4;     // pw row pitch (16-bit codes): 456-byte rows
+constexpr int MAXH = 64;          // heads of this kernel
+constexpr int MAXHM = 192;        // H * M of the per-neighbour bias store
+constexpr int BMW = 2 * MAXH + TQ * MAXHM;  // bias store: fp32 words
+constexpr int VRP = HD;           // V chunk row pitch (16-bit): 64-byte rows
+constexpr float LOG2E = 1.4426950408889634f;
+static_assert(WWORDS == THREADS, "one bitmap word per thread");
+static_assert(TQ * LPQ == THREADS, "one set-up lane group per query");
+static_assert((TQ * PWP) % 8 == 0, "pw is cleared in 16-byte pieces");
+static_assert(BMW * 4 < 65536, "bias-store byte offsets are 16-bit codes");
+}  // namespace wt
+
+// max / sum of v over lanes l and l ^ 32 (v_permlane32_swap exchanges the two halves)
+__device__ __forceinline__ float pair_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// The per-row routine over rows n0 .. n0 + nq - 1 of image b, every head, 4 lanes
+// per row (head_dim 32), 4 neighbours per block so that its registers stay
+// below the wave kernel's own.
+template <typename T, int BIAS>
+__device__ __forceinline__ void tile_rows(const aff_nbhd_attn_args &a, int b, int n0, int nq) {
+    const int sub = threadIdx.x & 3, rr = threadIdx.x >> 2;
+    for (int p = rr; p < nq * a.H; p += THREADS / 4) {
+        const int qq = p % nq, hd = p / nq;
+        if (n0 + qq < a.N) attend_row<T, 32, BIAS, 4>(a, b, hd, n0 + qq, sub);
+    }
+}
+
+template <typename T, int BIAS, bool IDX64, bool BLANK>
+__global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nbhd_attn_args a) {
+    using namespace wt;
+    using MM = Mfma32<T>;
+    // pw[q][slot]: byte offset in bm of the (query, neighbour) pair's biases; 0 (the
+    // -inf entry) where the union slot is not one of the query's neighbours
+    __shared__ __align__(16) uint16_t pw[TQ * PWP];
+    // bm: biases times log2(e): [H] -inf, [H] zero, then [TQ][M][H]
+    __shared__ __align__(16) float bm[BMW];
+    __shared__ int ulist[UMAX + 1];  // entry UMAX: sink of the set-up's dropped writes
+    struct SetupLds {
+        uint32_t bits[WWORDS];
+        uint32_t pref[WWORDS];
+        uint32_t qbits[TQ][UMAX / 32];
+    };
+    __shared__ __align__(16) union {
+        SetupLds s;
+        uint16_t vb[NW][32 * VRP];  // per-wave V chunk (head phase)
+    } sh;
+    __shared__ float nmq_s[TQ];
+    __shared__ int red[4];  // 0 flagged, 1 repeated index, 2 U
+
+    const int t = threadIdx.x, lane = t & 63;
+    const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: heads index scalar buffers
+    const int q = t >> 3, jl = t & 7;
+    const int N = a.N, M = a.M, H = a.H;
+    const int tiles = (N + TQ - 1) / TQ;
+    const int tile = int(xcd_swizzle(blockIdx.x, gridDim.x));
+    const int b = tile / tiles;
+    const int n0 = (tile % tiles) * TQ;
+    const int n = n0 + q;
+    const bool qlive = n < N;
+    const int nc = min(n, N - 1);
+
+    if (t < 4) red[t] = 0;
+    sh.s.bits[t] = 0;
+    for (int i = t; i < TQ * (UMAX / 32); i += THREADS) (&sh.s.qbits[0][0])[i] = 0;
+    for (int i = t; i < TQ * PWP / 8; i += THREADS) reinterpret_cast<uint4 *>(pw)[i] = make_uint4(0, 0, 0, 0);
+    if (t < H) {
+        bm[t] = -INFINITY;
+        bm[H + t] = 0.f;
+    }
+
+    // ---- this lane's (query, neighbour) entries j = jl + 8 r.  Loads are unconditional
+    // buffer loads at 32-bit offsets inside this image's planes (clamped to entry M - 1
+    // and row nc; the host keeps the offsets below 2^31), validity is a select.
+    auto rsrc = [](const void *p) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, -1, 0x00020000);
+    };
+    const int mlast = max(M - 1, 0);
+    const auto r_mi = rsrc(static_cast<const char *>(a.member_idx) + (int64_t)b * a.mi_sb * (IDX64 ? 8 : 4));
+    const uint32_t mi_off = uint32_t(nc) * uint32_t(a.mi_sn);
+    int idx[RJ];
+    bool use[RJ];
+    int nmask = 0;
+#pragma unroll
+    for (int r = 0; r < RJ; ++r) {
+        const int j = jl + LPQ * r, jc = min(j, mlast);
+        const bool live = qlive && j < M;
+        bool ok = false;
+        int ix = 0;
+        if (M > 0) {
+            if constexpr (IDX64) {
+                const auto v2 = __builtin_amdgcn_raw_buffer_load_b64(r_mi, int((mi_off + jc) * 8), 0, 0);
+                const int64_t v = int64_t(uint64_t(v2[0]) | (uint64_t(v2[1]) << 32));
+                ok = live && v >= 0 && v < N;
+                ix = int(v);
+            } else {
+                const int v = int(__builtin_amdgcn_raw_buffer_load_b32(r_mi, int((mi_off + jc) * 4), 0, 0));
+                ok = live && unsigned(v) < unsigned(N);
+                ix = v;
+            }
+        }
+        if (a.mask) {
+            const auto r_mk = rsrc(a.mask + (int64_t)b * a.mask_sb);
+            ok = ok && __builtin_amdgcn_raw_buffer_load_b8(r_mk, int(uint32_t(nc) * uint32_t(a.mask_sn) + jc), 0, 0) != 0;
+        }
+        use[r] = ok;
+        idx[r] = ok ? ix : nc;
+        nmask += (live && !ok) ? 1 : 0;
+    }
+
+    // ---- biases of the entries, every head, times log2(e), into bm
+    const int rowq_b = 2 * H + q * M * H;  // bm word of (q, j = 0, h = 0)
+    if constexpr (BIAS != 0) {
+        float pqx = 0.f, pqy = 0.f;
+        const float *pos_b = nullptr;
+        if constexpr (BIAS == 3 || BIAS == 4) {
+            pos_b = a.pos + (int64_t)b * a.pos_sb;
+            const float2 pq = *reinterpret_cast<const float2 *>(pos_b + (int64_t)nc * a.pos_sn);
+            pqx = pq.x;
+            pqy = pq.y;
+        }
+        const int Tw = 2 * a.rel_width + 1;
+#pragma unroll
+        for (int r = 0; r < RJ; ++r) {
+            if (!use[r]) continue;
+            const int j = jl + LPQ * r;
+            float *dst = bm + rowq_b + j * H;
+            int64_t row = -1;
+            if constexpr (BIAS == 2) {
+                const int64_t e = (int64_t)b * a.pe_sb + (int64_t)nc * a.pe_sn + j;
+                row = a.pe_is_i64 ? static_cast<const int64_t *>(a.pe_idx)[e]
+                                  : int64_t(static_cast<const int32_t *>(a.pe_idx)[e]);
+            } else if constexpr (BIAS == 4) {
+                const float2 g = *reinterpret_cast<const float2 *>(pos_b + (int64_t)idx[r] * a.pos_sn);
+                row = pe_from_coords32(pqx, pqy, g.x, g.y, float(a.rel_width), float(Tw));
+            }
+            if constexpr (BIAS == 2 || BIAS == 4) {
+                const bool in = row >= 0 && row < a.table_rows;
+                if (a.table_dtype == AFF_F32 && (H & 3) == 0) {
+                    const float4 *src = reinterpret_cast<const float4 *>(static_cast<const float *>(a.table) + (in ? row : 0) * H);
+                    for (int h = 0; h < H; h += 4) {
+                        const float4 v = src[h >> 2];
+                        const float sc = in ? LOG2E : 0.f;
+                        *reinterpret_cast<float4 *>(dst + h) = make_float4(v.x * sc, v.y * sc, v.z * sc, v.w * sc);
+                    }
+                } else {
+                    for (int h = 0; h < H; ++h)
+                        dst[h] = in ? load_any(a.table, a.table_dtype, row * H + h) * LOG2E : 0.f;
+                }
+            } else if constexpr (BIAS == 1) {
+                const int64_t e = (int64_t)b * a.bias_sb + (int64_t)nc * a.bias_sn + j;
+                for (int h = 0; h < H; ++h)
+                    dst[h] = load_any(a.bias, a.bias_dtype, e + (int64_t)h * a.bias_sh) * LOG2E;
+            } else if constexpr (BIAS == 3) {
+                const float2 g = *reinterpret_cast<const float2 *>(pos_b + (int64_t)idx[r] * a.pos_sn);
+                for (int h = 0; h < H; ++h)
+                    dst[h] = cont_bias(a.pos_w + h * 5, a.pos_b[h], g.x - pqx, g.y - pqy) * LOG2E;
+            }
+        }
+    }
+    // the cleared bitmap and counters are visible before any wave's atomics
+    // (the loads above stay in flight across this barrier)
+    lds_barrier();
+
+    // ---- union bitmap over the index window [wlo, wlo + 8192)
+    const int wlo = max(0, min(n0 + TQ / 2 - WWORDS * 16, N - WWORDS * 32));
+    bool outside = false;
+#pragma unroll
+    for (int r = 0; r < RJ; ++r) {
+        const unsigned o = unsigned(idx[r] - wlo);
+        const bool in = o < unsigned(WWORDS * 32);
+        outside = outside || (use[r] && !in);
+        const unsigned oc = in ? o : 0u;
+        atomicOr(&sh.s.bits[oc >> 5], (use[r] && in) ? 1u << (oc & 31) : 0u);
+    }
+    if (outside) red[0] = 1;
+    {
+        const float nm = grp8_sum(float(nmask));
+        if (jl == 0) nmq_s[q] = nm;
+    }
+    lds_barrier();
+
+    const bool flagged = (a.mask && a.mask_sh != 0) || red[0] != 0;
+    if (!flagged && w == 0) {
+        uint32_t c[4];
+        int tot = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            c[i] = __popc(sh.s.bits[lane * 4 + i]);
+            tot += c[i];
+        }
+        int inc = tot;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(inc, o, 64);
+            if (lane >= o) inc += v;
+        }
+        int ex = inc - tot;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sh.s.pref[lane * 4 + i] = ex;
+            ex += c[i];
+        }
+        if (lane == 63) red[2] = inc;
+    }
+    lds_barrier();
+    const int U = red[2];
+    bool fallback = flagged || U > UMAX;
+
+    if (!fallback) {
+        const int rowq = q * PWP;
+        const uint32_t zero_code = uint32_t(H) * 4;  // byte offset of the zero entry
+#pragma unroll
+        for (int r = 0; r < RJ; ++r) {
+            const int o = min(max(idx[r] - wlo, 0), WWORDS * 32 - 1), wd = o >> 5, bt = o & 31;
+            const int s = int(sh.s.pref[wd] + __popc(sh.s.bits[wd] & ((1u << bt) - 1u)));
+            const bool u = use[r];
+            ulist[u ? s : UMAX] = idx[r];
+            const uint32_t bit = u ? 1u << (s & 31) : 0u;
+            if (atomicOr(&sh.s.qbits[q][u ? (s >> 5) : 0], bit) & bit) red[1] = 1;  // repeated index
+            const uint32_t code = BIAS == 0 ? zero_code : uint32_t(rowq_b + (jl + LPQ * r) * H) * 4;
+            pw[u ? rowq + s : rowq + UMAX + 1] = uint16_t(code);
+        }
+    }
+    lds_barrier();
+    fallback = fallback || red[1] != 0;
+
+    if (fallback) {
+        tile_rows<T, BIAS>(a, b, n0, TQ);
+        return;
+    }
+
+    // ---- head phase: wave w, heads w, w + NW, ...
+    const int hh = lane >> 5, ql = lane & 31;
+    const int nch = (U + 31) >> 5;
+    const bool qout = n0 + ql < N;
+    const int qrow = min(n0 + ql, N - 1);
+    const float nm = nmq_s[ql];
+    const uint32_t ksn2 = uint32_t(a.k_sn * 2), vsn2 = uint32_t(a.v_sn * 2);  // < 2^24, host-checked
+    const uint32_t qoff = uint32_t(qrow) * uint32_t(a.q_sn * 2) + 32 * hh;
+    const float scale2 = a.scale * LOG2E;
+    // transposing-read role: 16-lane group g reads channels 16 (g & 1) + (lane & 15)
+    const int kk = (lane & 15) >> 2, aa = lane & 3, cg = 16 * ((lane >> 4) & 1);
+    uint16_t *vbuf = sh.vb[w];
+    const uint16_t *pwrow = pw + ql * PWP + 4 * hh;
+    const uint32_t vst0 = (lane >> 2) * VRP + (lane & 3) * 8, vst1 = vst0 + 16 * VRP;
+    const uint16_t *vtr = vbuf + (4 * hh + kk) * VRP + cg + 4 * aa;
+    // K row of this lane in chunk c: union slot 32 c + ql; V pieces p = lane + 64 i: row p >> 2, bytes 16 (p & 3)
+    auto koff = [&](int c) {
+        const int s = 32 * c + ql;
+        return __umul24(uint32_t(ulist[s < U ? s : 0]), ksn2) + 32 * hh;
+    };
+    auto voff = [&](int c, int i) {
+        const int s = 32 * c + 16 * i + (lane >> 2);
+        return __umul24(uint32_t(ulist[s < U ? s : 0]), vsn2) + 16 * (lane & 3);
+    };
+    auto ld = [](__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+        return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, int(off), 0, 0));
+    };
+
+    for (int h = w; h < H; h += NW) {
+        const auto rq = rsrc(static_cast<const char *>(a.q) + ((int64_t)b * a.q_sb + (int64_t)h * a.q_sh) * 2);
+        const auto rk = rsrc(static_cast<const char *>(a.k) + ((int64_t)b * a.k_sb + (int64_t)h * a.k_sh) * 2);
+        const auto rv = rsrc(static_cast<const char *>(a.v) + ((int64_t)b * a.v_sb + (int64_t)h * a.v_sh) * 2);
+        // K/V registers of two chunks: chunk c + 1 loads while chunk c computes
+        uint4 kA0 = make_uint4(0, 0, 0, 0), kA1 = kA0, vA0 = kA0, vA1 = kA0;
+        uint4 kB0 = kA0, kB1 = kA0, vB0 = kA0, vB1 = kA0;
+        auto fetch = [&](int c, uint4 &k0, uint4 &k1, uint4 &v0, uint4 &v1) {
+            const uint32_t ko = koff(c);
+            k0 = ld(rk, ko);
+            k1 = ld(rk, ko + 16);
+            v0 = ld(rv, voff(c, 0));
+            v1 = ld(rv, voff(c, 1));
+        };
+        if (nch > 0) fetch(0, kA0, kA1, vA0, vA1);
+        const uint4 q0 = ld(rq, qoff), q1 = ld(rq, qoff + 16);
+        float m = MASKED_LOGIT * LOG2E;
+        float sb = 0.f;
+        if constexpr (BLANK) {
+            const char *bkp = static_cast<const char *>(a.blank_k) + (h * HD + 16 * hh) * 2;
+            const uint4 bk0 = *reinterpret_cast<const uint4 *>(bkp), bk1 = *reinterpret_cast<const uint4 *>(bkp + 16);
+            const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+            const uint32_t kw[8] = {bk0.x, bk0.y, bk0.z, bk0.w, bk1.x, bk1.y, bk1.z, bk1.w};
+            float part = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                part += MM::to_f32(uint16_t(qw[e] & 0xffffu)) * MM::to_f32(uint16_t(kw[e] & 0xffffu)) +
+                        MM::to_f32(uint16_t(qw[e] >> 16)) * MM::to_f32(uint16_t(kw[e] >> 16));
+            sb = pair_sum(part) * scale2;
+            m = fmaxf(m, sb);
+        }
+        const char *bmh = reinterpret_cast<const char *>(bm) + 4 * h;
+        float lp = 0.f;
+        f32x16 O;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) O[r] = 0.f;
+
+        auto chunk = [&](int c, const uint4 &k0, const uint4 &k1, const uint4 &v0, const uint4 &v1) {
+            // bias of this lane's 16 slots (8 j + 4 hh + i of the chunk): code, then value
+            uint32_t cw[8];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint2 v = *reinterpret_cast<const uint2 *>(pwrow + 32 * c + 8 * j);
+                cw[2 * j] = v.x;
+                cw[2 * j + 1] = v.y;
+            }
+            float bias[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t code = (r & 1) ? (cw[r >> 1] >> 16) : (cw[r >> 1] & 0xffffu);
+                bias[r] = *reinterpret_cast<const float *>(bmh + code);
+            }
+            f32x16 S;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) S[r] = 0.f;
+            S = MM::mma(k0, q0, S);
+            S = MM::mma(k1, q1, S);
+            float x[16];
+            float cm = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                x[r] = fmaf(S[r], scale2, bias[r]);
+                cm = fmaxf(cm, x[r]);
+            }
+            // the running maximum moves only when a logit exceeds it by more than 8
+            // (probabilities then stay below 2^8), so the rescale is rare
+            const float cmp = pair_max(cm);
+            if (__builtin_amdgcn_ballot_w64(cmp > m + 8.f) != 0) {
+                const float mn = fmaxf(m, cmp);
+                const float alpha = __builtin_amdgcn_exp2f(m - mn);
+                m = mn;
+                lp *= alpha;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) O[r] *= alpha;
+            }
+            float ps = 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                x[r] = __builtin_amdgcn_exp2f(x[r] - m);
+                ps += x[r];
+            }
+            lp += ps;
+            // this chunk's V rows into the wave's buffer (its previous reads are done: LDS
+            // operations of one wave complete in order)
+            asm volatile("" ::: "memory");
+            *reinterpret_cast<uint4 *>(vbuf + vst0) = v0;
+            *reinterpret_cast<uint4 *>(vbuf + vst1) = v1;
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int mm = 0; mm < 2; ++mm) {
+                const uint2 va = lds_read_tr16(vtr + (16 * mm) * VRP);
+                const uint2 vc = lds_read_tr16(vtr + (16 * mm + 8) * VRP);
+                const uint4 pb = make_uint4(MM::pack2(x[8 * mm + 0], x[8 * mm + 1]), MM::pack2(x[8 * mm + 2], x[8 * mm + 3]),
+                                            MM::pack2(x[8 * mm + 4], x[8 * mm + 5]), MM::pack2(x[8 * mm + 6], x[8 * mm + 7]));
+                O = MM::mma(make_uint4(va.x, va.y, vc.x, vc.y), pb, O);
+            }
+        };
+
+        // The fetches are unconditional (past the last chunk they re-read it): a
+        // conditional load would make the compiler wait for it before the current
+        // chunk's MFMAs on every path, serialising load latency with compute.
+        for (int c = 0; c < nch; c += 2) {
+            fetch(min(c + 1, nch - 1), kB0, kB1, vB0, vB1);
+            chunk(c, kA0, kA1, vA0, vA1);
+            if (c + 1 >= nch) break;
+            fetch(min(c + 2, nch - 1), kA0, kA1, vA0, vA1);
+            chunk(c + 1, kB0, kB1, vB0, vB1);
+        }
+
+        // ---- normalise, blank value, store: channels 8 j + 4 hh + i of query ql
+        const float pbl = BLANK ? __builtin_amdgcn_exp2f(sb - m) : 0.f;
+        const float l = pair_sum(lp) + pbl + (nm > 0.f ? nm * __builtin_amdgcn_exp2f(MASKED_LOGIT * LOG2E - m) : 0.f);
+        const float inv = __builtin_amdgcn_rcpf(l + 1e-12f);  // 1 ulp: outputs are 16-bit
+        if (qout) {
+            T *orow = static_cast<T *>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)(n0 + ql) * a.o_sn;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int d0 = 8 * j + 4 * hh;
+                float y[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) y[i] = O[4 * j + i];
+                if constexpr (BLANK) {
+                    const uint2 bv = *reinterpret_cast<const uint2 *>(static_cast<const char *>(a.blank_v) + (h * HD + d0) * 2);
+                    y[0] += pbl * MM::to_f32(uint16_t(bv.x & 0xffffu));
+                    y[1] += pbl * MM::to_f32(uint16_t(bv.x >> 16));
+                    y[2] += pbl * MM::to_f32(uint16_t(bv.y & 0xffffu));
+                    y[3] += pbl * MM::to_f32(uint16_t(bv.y >> 16));
+                }
+                *reinterpret_cast<uint2 *>(orow + d0) =
+                    make_uint2(MM::pack2(y[0] * inv, y[1] * inv), MM::pack2(y[2] * inv, y[3] * inv));
+            }
+            if (a.lse && hh == 0) a.lse[((int64_t)b * H + h) * N + n0 + ql] = m * 0.6931471805599453f + __logf(l + 1e-12f);
+        }
+    }
+}
+
 using KernelFn = void (*)(const aff_nbhd_attn_args);
 
 template <typename T, int D>
@@ -787,6 +1272,41 @@ inline int64_t tile_count(const aff_nbhd_attn_args &a) {
     return (int64_t)a.B * ((a.N + tile::TQ - 1) / tile::TQ);
 }
 
+// The wave-per-head kernel: the tile path's conditions, bias modes 0, 2, 4 with
+// table rows that fit its 16-bit codes, at most 256 heads.
+inline bool use_wave_path(const aff_nbhd_attn_args &a) {
+    if (a.dtype == AFF_F32 || a.D != wt::HD || a.M > wt::MAXM) return false;
+    if (a.H > wt::MAXH || (int64_t)a.H * a.M > wt::MAXHM) return false;
+    // 32-bit byte offsets inside one (b, h) plane, built with 24-bit multiplies
+    auto plane_ok = [&](int64_t sn) {
+        return sn >= 0 && sn * 2 < ((int64_t)1 << 24) && ((int64_t)(a.N - 1) * sn + a.D) * 2 < ((int64_t)1 << 32);
+    };
+    if (!(a.N < (1 << 24) && plane_ok(a.q_sn) && plane_ok(a.k_sn) && plane_ok(a.v_sn))) return false;
+    // set-up loads use 32-bit byte offsets inside one image's index and mask planes
+    const int64_t lim = (int64_t)1 << 31;
+    if (a.mi_sn < 0 || ((int64_t)a.N * a.mi_sn + a.M) * 8 >= lim) return false;
+    if (a.mask && (a.mask_sn < 0 || (int64_t)a.N * a.mask_sn + a.M >= lim)) return false;
+    return true;
+}
+
+template <typename T, int BIAS>
+KernelFn pick_wave3(bool i64, bool blank) {
+    if (i64) return blank ? nbhd_attn_wave_kernel<T, BIAS, true, true> : nbhd_attn_wave_kernel<T, BIAS, true, false>;
+    return blank ? nbhd_attn_wave_kernel<T, BIAS, false, true> : nbhd_attn_wave_kernel<T, BIAS, false, false>;
+}
+
+template <typename T>
+KernelFn pick_wave(const aff_nbhd_attn_args &a) {
+    const bool i64 = a.idx_is_i64 != 0, blank = a.blank_k != nullptr;
+    switch (a.bias_mode) {
+        case 0: return pick_wave3<T, 0>(i64, blank);
+        case 1: return pick_wave3<T, 1>(i64, blank);
+        case 2: return pick_wave3<T, 2>(i64, blank);
+        case 3: return pick_wave3<T, 3>(i64, blank);
+        default: return pick_wave3<T, 4>(i64, blank);
+    }
+}
+
 }  // namespace attn
 }  // namespace aff
 
@@ -794,6 +1314,7 @@ using namespace aff;
 
 extern "C" size_t aff_nbhd_attn_workspace_bytes(const aff_nbhd_attn_args *args) {
     if (args == nullptr || (int64_t)args->B * args->H * args->N == 0) return 0;
+    if (attn::use_wave_path(*args)) return 0;
     return attn::use_tile_path(*args) ? (size_t)attn::tile_count(*args) : 0;
 }
 
@@ -836,6 +1357,13 @@ extern "C" aff_status aff_nbhd_attn_fwd(const aff_nbhd_attn_args *args, aff_stre
     }
     hipStream_t hs = static_cast<hipStream_t>(stream);
 
+    if (attn::use_wave_path(a)) {
+        const int64_t ntiles = attn::tile_count(a);
+        AFF_CHECK_ARG(ntiles < (int64_t)1 << 31, "aff_nbhd_attn_fwd: problem too large");
+        const attn::KernelFn fn = a.dtype == AFF_BF16 ? attn::pick_wave<bf16_t>(a) : attn::pick_wave<f16_t>(a);
+        hipLaunchKernelGGL(fn, dim3((unsigned)ntiles), dim3(attn::THREADS), 0, hs, a);
+        return check_launch("aff_nbhd_attn_fwd (wave tiles)");
+    }
     if (attn::use_tile_path(a)) {
         const int64_t ntiles = attn::tile_count(a);
         AFF_CHECK_ARG(ntiles < (int64_t)1 << 31, "aff_nbhd_attn_fwd: problem too large");
