@@ -843,11 +843,11 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
     __shared__ __align__(16) uint16_t pw[TQ * PWP];
     // bm: biases times log2(e): [H] -inf, [H] zero, then [TQ][M][H]
     __shared__ __align__(16) float bm[BMW];
-    __shared__ int ulist[UMAX + 1];  // entry UMAX: sink of the set-up's dropped writes
+    __shared__ int ulist[UMAX];
     struct SetupLds {
-        uint32_t bits[WWORDS];
-        uint32_t pref[WWORDS];
-        uint32_t qbits[TQ][UMAX / 32];
+        uint8_t flg[WWORDS * 32];  // one byte per index of the window: a neighbour row
+        uint32_t bits[WWORDS];     // the same flags packed 32 to a word
+        uint32_t pref[WWORDS];     // union slots before each word
     };
     __shared__ __align__(16) union {
         SetupLds s;
@@ -867,10 +867,10 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
     const int n = n0 + q;
     const bool qlive = n < N;
     const int nc = min(n, N - 1);
+    const int nr = (M + LPQ - 1) / LPQ;  // entries per set-up lane that exist (uniform)
 
     if (t < 4) red[t] = 0;
-    sh.s.bits[t] = 0;
-    for (int i = t; i < TQ * (UMAX / 32); i += THREADS) (&sh.s.qbits[0][0])[i] = 0;
+    for (int i = t; i < WWORDS * 2; i += THREADS) reinterpret_cast<uint4 *>(sh.s.flg)[i] = make_uint4(0, 0, 0, 0);
     for (int i = t; i < TQ * PWP / 8; i += THREADS) reinterpret_cast<uint4 *>(pw)[i] = make_uint4(0, 0, 0, 0);
     if (t < H) {
         bm[t] = -INFINITY;
@@ -891,21 +891,22 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
     int nmask = 0;
 #pragma unroll
     for (int r = 0; r < RJ; ++r) {
+        use[r] = false;
+        idx[r] = nc;
+        if (r >= nr) continue;
         const int j = jl + LPQ * r, jc = min(j, mlast);
         const bool live = qlive && j < M;
-        bool ok = false;
-        int ix = 0;
-        if (M > 0) {
-            if constexpr (IDX64) {
-                const auto v2 = __builtin_amdgcn_raw_buffer_load_b64(r_mi, int((mi_off + jc) * 8), 0, 0);
-                const int64_t v = int64_t(uint64_t(v2[0]) | (uint64_t(v2[1]) << 32));
-                ok = live && v >= 0 && v < N;
-                ix = int(v);
-            } else {
-                const int v = int(__builtin_amdgcn_raw_buffer_load_b32(r_mi, int((mi_off + jc) * 4), 0, 0));
-                ok = live && unsigned(v) < unsigned(N);
-                ix = v;
-            }
+        bool ok;
+        int ix;
+        if constexpr (IDX64) {
+            const auto v2 = __builtin_amdgcn_raw_buffer_load_b64(r_mi, int((mi_off + jc) * 8), 0, 0);
+            const int64_t v = int64_t(uint64_t(v2[0]) | (uint64_t(v2[1]) << 32));
+            ok = live && v >= 0 && v < N;
+            ix = int(v);
+        } else {
+            const int v = int(__builtin_amdgcn_raw_buffer_load_b32(r_mi, int((mi_off + jc) * 4), 0, 0));
+            ok = live && unsigned(v) < unsigned(N);
+            ix = v;
         }
         if (a.mask) {
             const auto r_mk = rsrc(a.mask + (int64_t)b * a.mask_sb);
@@ -916,8 +917,18 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
         nmask += (live && !ok) ? 1 : 0;
     }
 
-    // ---- biases of the entries, every head, times log2(e), into bm
+    // ---- biases of the entries, every head, times log2(e), for bm.  The usual case
+    // (fp32 table, 4 heads) keeps the table rows in flight in registers until the
+    // union is built; the others store at once.
     const int rowq_b = 2 * H + q * M * H;  // bm word of (q, j = 0, h = 0)
+    const bool fast4 = (BIAS == 2 || BIAS == 4) && H == 4 && a.table_dtype == AFF_F32;
+    float4 tv[RJ];
+    bool tin[RJ];
+#pragma unroll
+    for (int r = 0; r < RJ; ++r) {
+        tv[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+        tin[r] = false;
+    }
     if constexpr (BIAS != 0) {
         float pqx = 0.f, pqy = 0.f;
         const float *pos_b = nullptr;
@@ -930,7 +941,7 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
         const int Tw = 2 * a.rel_width + 1;
 #pragma unroll
         for (int r = 0; r < RJ; ++r) {
-            if (!use[r]) continue;
+            if (r >= nr || !use[r]) continue;
             const int j = jl + LPQ * r;
             float *dst = bm + rowq_b + j * H;
             int64_t row = -1;
@@ -944,47 +955,69 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
             }
             if constexpr (BIAS == 2 || BIAS == 4) {
                 const bool in = row >= 0 && row < a.table_rows;
-                if (a.table_dtype == AFF_F32 && (H & 3) == 0) {
-                    const float4 *src = reinterpret_cast<const float4 *>(static_cast<const float *>(a.table) + (in ? row : 0) * H);
-                    for (int h = 0; h < H; h += 4) {
-                        const float4 v = src[h >> 2];
-                        const float sc = in ? LOG2E : 0.f;
-                        *reinterpret_cast<float4 *>(dst + h) = make_float4(v.x * sc, v.y * sc, v.z * sc, v.w * sc);
-                    }
+                if (fast4) {
+                    tin[r] = in;
+                    tv[r] = reinterpret_cast<const float4 *>(a.table)[in ? row : 0];
                 } else {
                     for (int h = 0; h < H; ++h)
                         dst[h] = in ? load_any(a.table, a.table_dtype, row * H + h) * LOG2E : 0.f;
                 }
             } else if constexpr (BIAS == 1) {
                 const int64_t e = (int64_t)b * a.bias_sb + (int64_t)nc * a.bias_sn + j;
-                for (int h = 0; h < H; ++h)
-                    dst[h] = load_any(a.bias, a.bias_dtype, e + (int64_t)h * a.bias_sh) * LOG2E;
+                for (int h = 0; h < H; ++h) dst[h] = load_any(a.bias, a.bias_dtype, e + (int64_t)h * a.bias_sh) * LOG2E;
             } else if constexpr (BIAS == 3) {
                 const float2 g = *reinterpret_cast<const float2 *>(pos_b + (int64_t)idx[r] * a.pos_sn);
-                for (int h = 0; h < H; ++h)
-                    dst[h] = cont_bias(a.pos_w + h * 5, a.pos_b[h], g.x - pqx, g.y - pqy) * LOG2E;
+                for (int h = 0; h < H; ++h) dst[h] = cont_bias(a.pos_w + h * 5, a.pos_b[h], g.x - pqx, g.y - pqy) * LOG2E;
             }
         }
+    } else {
+        // no bias: zero entries, so that every (query, neighbour) pair still has its own code
+#pragma unroll
+        for (int r = 0; r < RJ; ++r)
+            if (r < nr && use[r])
+                for (int h = 0; h < H; ++h) bm[rowq_b + (jl + LPQ * r) * H + h] = 0.f;
     }
-    // the cleared bitmap and counters are visible before any wave's atomics
-    // (the loads above stay in flight across this barrier)
+    // the cleared flags are visible before any wave sets one (the loads above stay
+    // in flight across this barrier)
     lds_barrier();
 
-    // ---- union bitmap over the index window [wlo, wlo + 8192)
+    // ---- union: a flag byte per neighbour row of the index window [wlo, wlo + 8192)
+    // (plain stores: every writer of a byte writes the same 1)
     const int wlo = max(0, min(n0 + TQ / 2 - WWORDS * 16, N - WWORDS * 32));
     bool outside = false;
 #pragma unroll
     for (int r = 0; r < RJ; ++r) {
+        if (r >= nr) continue;
         const unsigned o = unsigned(idx[r] - wlo);
         const bool in = o < unsigned(WWORDS * 32);
         outside = outside || (use[r] && !in);
-        const unsigned oc = in ? o : 0u;
-        atomicOr(&sh.s.bits[oc >> 5], (use[r] && in) ? 1u << (oc & 31) : 0u);
+        if (use[r] && in) sh.s.flg[o] = 1;
     }
     if (outside) red[0] = 1;
     {
         const float nm = grp8_sum(float(nmask));
         if (jl == 0) nmq_s[q] = nm;
+    }
+    lds_barrier();
+
+    // ---- flags -> bits (thread t packs window word t); the biases held in registers -> bm
+    {
+        const uint4 f0 = reinterpret_cast<const uint4 *>(sh.s.flg)[2 * t];
+        const uint4 f1 = reinterpret_cast<const uint4 *>(sh.s.flg)[2 * t + 1];
+        const uint32_t d[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+        uint32_t wbits = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) wbits |= (((d[k] * 0x01020408u) >> 24) & 0xFu) << (4 * k);  // 4 flag bytes -> 4 bits
+        sh.s.bits[t] = wbits;
+    }
+    if (fast4) {
+#pragma unroll
+        for (int r = 0; r < RJ; ++r)
+            if (r < nr && use[r]) {
+                const float sc = tin[r] ? LOG2E : 0.f;
+                *reinterpret_cast<float4 *>(bm + rowq_b + (jl + LPQ * r) * 4) =
+                    make_float4(tv[r].x * sc, tv[r].y * sc, tv[r].z * sc, tv[r].w * sc);
+            }
     }
     lds_barrier();
 
@@ -1015,23 +1048,36 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
     const int U = red[2];
     bool fallback = flagged || U > UMAX;
 
+    // ---- union slots; pw codes (plain stores: a code is unique to its (query, neighbour)
+    // entry, so a repeated index within one query shows up as an overwritten code)
+    int slot[RJ];
     if (!fallback) {
         const int rowq = q * PWP;
-        const uint32_t zero_code = uint32_t(H) * 4;  // byte offset of the zero entry
 #pragma unroll
         for (int r = 0; r < RJ; ++r) {
+            slot[r] = 0;
+            if (r >= nr) continue;
             const int o = min(max(idx[r] - wlo, 0), WWORDS * 32 - 1), wd = o >> 5, bt = o & 31;
-            const int s = int(sh.s.pref[wd] + __popc(sh.s.bits[wd] & ((1u << bt) - 1u)));
-            const bool u = use[r];
-            ulist[u ? s : UMAX] = idx[r];
-            const uint32_t bit = u ? 1u << (s & 31) : 0u;
-            if (atomicOr(&sh.s.qbits[q][u ? (s >> 5) : 0], bit) & bit) red[1] = 1;  // repeated index
-            const uint32_t code = BIAS == 0 ? zero_code : uint32_t(rowq_b + (jl + LPQ * r) * H) * 4;
-            pw[u ? rowq + s : rowq + UMAX + 1] = uint16_t(code);
+            const int s_ = int(sh.s.pref[wd] + __popc(sh.s.bits[wd] & ((1u << bt) - 1u)));
+            slot[r] = s_;
+            if (use[r]) {
+                ulist[s_] = idx[r];
+                pw[rowq + s_] = uint16_t(uint32_t(rowq_b + (jl + LPQ * r) * H) * 4);
+            }
         }
     }
     lds_barrier();
-    fallback = fallback || red[1] != 0;
+    if (!fallback) {
+        bool dup = false;
+        const int rowq = q * PWP;
+#pragma unroll
+        for (int r = 0; r < RJ; ++r)
+            if (r < nr && use[r])
+                dup = dup || pw[rowq + slot[r]] != uint16_t(uint32_t(rowq_b + (jl + LPQ * r) * H) * 4);
+        if (__builtin_amdgcn_ballot_w64(dup) != 0 && lane == 0) red[1] = 1;
+        lds_barrier();
+        fallback = red[1] != 0;
+    }
 
     if (fallback) {
         tile_rows<T, BIAS>(a, b, n0, TQ);
