@@ -1149,21 +1149,46 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
 #pragma unroll
         for (int r = 0; r < 16; ++r) O[r] = 0.f;
 
-        auto chunk = [&](int c, const uint4 &k0, const uint4 &k1, const uint4 &v0, const uint4 &v1) {
-            // bias of this lane's 16 slots (8 j + 4 hh + i of the chunk): code, then value
-            uint32_t cw[8];
+        // LDS data of the lane's 16 slots (8 j + 4 hh + i of a chunk): the codes are read
+        // two chunks ahead and the biases one chunk ahead of their use
+        auto read_codes = [&](int c, uint32_t (&cw)[8]) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const uint2 v = *reinterpret_cast<const uint2 *>(pwrow + 32 * c + 8 * j);
                 cw[2 * j] = v.x;
                 cw[2 * j + 1] = v.y;
             }
-            float bias[16];
+        };
+        auto read_bias = [&](const uint32_t (&cw)[8], float (&bias)[16]) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const uint32_t code = (r & 1) ? (cw[r >> 1] >> 16) : (cw[r >> 1] & 0xffffu);
                 bias[r] = *reinterpret_cast<const float *>(bmh + code);
             }
+        };
+        uint32_t cwA[8], cwB[8];
+        float bA[16], bB[16];
+        if (nch > 0) {
+            read_codes(0, cwA);
+            read_bias(cwA, bA);
+            read_codes(min(1, nch - 1), cwB);
+        }
+
+        // chunk c: K/V registers k0..v1, biases bc; codes of chunk c + 1 in cn (their
+        // biases go to bn) and the codes of chunk c + 2 replace cc
+        auto chunk = [&](int c, const uint4 &k0, const uint4 &k1, const uint4 &v0, const uint4 &v1, const float (&bc)[16],
+                         uint32_t (&cc)[8], const uint32_t (&cn)[8], float (&bn)[16]) {
+            // this chunk's V rows into the wave's buffer and their transposed reads (the
+            // previous chunk's reads are done: LDS operations of one wave complete in order)
+            asm volatile("" ::: "memory");
+            *reinterpret_cast<uint4 *>(vbuf + vst0) = v0;
+            *reinterpret_cast<uint4 *>(vbuf + vst1) = v1;
+            asm volatile("" ::: "memory");
+            uint2 vt[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) vt[i] = lds_read_tr16(vtr + (8 * i) * VRP);
+            read_bias(cn, bn);
+            read_codes(min(c + 2, nch - 1), cc);
             f32x16 S;
 #pragma unroll
             for (int r = 0; r < 16; ++r) S[r] = 0.f;
@@ -1173,7 +1198,7 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
             float cm = -INFINITY;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                x[r] = fmaf(S[r], scale2, bias[r]);
+                x[r] = fmaf(S[r], scale2, bc[r]);
                 cm = fmaxf(cm, x[r]);
             }
             // the running maximum moves only when a logit exceeds it by more than 8
@@ -1194,19 +1219,11 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
                 ps += x[r];
             }
             lp += ps;
-            // this chunk's V rows into the wave's buffer (its previous reads are done: LDS
-            // operations of one wave complete in order)
-            asm volatile("" ::: "memory");
-            *reinterpret_cast<uint4 *>(vbuf + vst0) = v0;
-            *reinterpret_cast<uint4 *>(vbuf + vst1) = v1;
-            asm volatile("" ::: "memory");
 #pragma unroll
             for (int mm = 0; mm < 2; ++mm) {
-                const uint2 va = lds_read_tr16(vtr + (16 * mm) * VRP);
-                const uint2 vc = lds_read_tr16(vtr + (16 * mm + 8) * VRP);
                 const uint4 pb = make_uint4(MM::pack2(x[8 * mm + 0], x[8 * mm + 1]), MM::pack2(x[8 * mm + 2], x[8 * mm + 3]),
                                             MM::pack2(x[8 * mm + 4], x[8 * mm + 5]), MM::pack2(x[8 * mm + 6], x[8 * mm + 7]));
-                O = MM::mma(make_uint4(va.x, va.y, vc.x, vc.y), pb, O);
+                O = MM::mma(make_uint4(vt[2 * mm].x, vt[2 * mm].y, vt[2 * mm + 1].x, vt[2 * mm + 1].y), pb, O);
             }
         };
 
@@ -1215,10 +1232,10 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
         // chunk's MFMAs on every path, serialising load latency with compute.
         for (int c = 0; c < nch; c += 2) {
             fetch(min(c + 1, nch - 1), kB0, kB1, vB0, vB1);
-            chunk(c, kA0, kA1, vA0, vA1);
+            chunk(c, kA0, kA1, vA0, vA1, bA, cwA, cwB, bB);
             if (c + 1 >= nch) break;
             fetch(min(c + 2, nch - 1), kA0, kA1, vA0, vA1);
-            chunk(c + 1, kB0, kB1, vB0, vB1);
+            chunk(c + 1, kB0, kB1, vB0, vB1, bB, cwB, cwA, bA);
         }
 
         // ---- normalise, blank value, store: channels 8 j + 4 hh + i of query ql
