@@ -347,8 +347,8 @@ __global__ __launch_bounds__(QUERY_THREADS) void knn_query_kernel(const float *_
 
 // ------------------------------------------------------- windowed kernel --
 constexpr int WIN_THREADS = 64;
-constexpr int WMAX = 1024;      // window points held in LDS
-constexpr int WCMAX = 640;      // window cell-offset entries, (WX + 1) * WY
+constexpr int WMAX = 640;       // window points held in LDS
+constexpr int WCMAX = 320;      // window cell-offset entries, (WX + 1) * WY
 constexpr int WROWS = 64;       // window rows (one lane each while sizing)
 constexpr float WIN_U = 1.6f;   // window disk: radius^2 = WIN_U * the initial estimate
 constexpr int MAX_SLOT = 65536; // 16-bit candidate slots
@@ -471,7 +471,7 @@ __global__ __launch_bounds__(WIN_THREADS) void knn_win_kernel(const float4 *__re
                                                               void *__restrict__ out_idx, int idx_i64,
                                                               float *__restrict__ out_d2) {
     __shared__ float2 s_xy[WMAX + 3];  // + spare entries read (and ignored) by the 4-wide visits
-    __shared__ int s_id[WMAX];
+    __shared__ uint16_t s_id[WMAX];  // point indices (the windowed path takes N <= 65536)
     __shared__ int s_wcs[WCMAX];
     __shared__ int s_rb[WROWS + 1];
     __shared__ int s_gb[WROWS];
@@ -538,7 +538,7 @@ __global__ __launch_bounds__(WIN_THREADS) void knn_win_kernel(const float4 *__re
                 while (s_rb[r + 1] <= t) ++r;
                 const float4 pt = g.P[s_gb[r] + (t - s_rb[r])];
                 s_xy[t] = make_float2(pt.x, pt.y);
-                s_id[t] = __float_as_int(pt.z);
+                s_id[t] = uint16_t(__float_as_int(pt.z));
             }
             __syncthreads();
         }
