@@ -23,7 +23,7 @@ AFF_ERR_LAUNCH = 4
 AFF_F32, AFF_F16, AFF_BF16 = 0, 1, 2
 DTYPE_CODE = {torch.float32: AFF_F32, torch.float16: AFF_F16, torch.bfloat16: AFF_BF16}
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 P = ctypes.c_void_p
 I32 = ctypes.c_int
@@ -96,6 +96,8 @@ SIGNATURES = {
                                     P, I32, I64, I64, P, I32, I64, I64, I32, P, I64, I64, P, I32, I64, I64, P]),
     "aff_msdetrpc_fwd": (I32, [P, I32, I64, I64, I64, P, I32, I64, I64, I64, P, I32, I64, I64, P, I32, I64, I64,
                                I32, I32, I32, I32, I32, I32, P, I64, I64, P]),
+    "aff_cluster_members": (I32, [P, I32, I64, I64, P, I32, I64, I64, P, I64, I64, P, I64, I64,
+                                  I32, I32, I32, I32, I32, I32, P, I32, P, P, I32, P]),
 }
 
 _lib = None

@@ -23,3 +23,4 @@ from .fused_deform_attn import (  # noqa: F401
 )
 from .msdetrpc import MSDETRPCFunction, launch_msdetrpc_forward  # noqa: F401
 from .mssample import mssample, MSSampleFunction  # noqa: F401
+from .nbhd_index import cluster_members  # noqa: F401

@@ -1,4 +1,9 @@
-"""AFF downsampling layer with the reference's signature (src/layers/aff.py:122-299).
+"""AFF layer pieces with the reference's signatures (src/layers/aff.py).
+
+``neighbourhood_index`` is the index construction of BasicLayer.forward
+(aff.py:414-465): space-filling clustering, nearest-cluster KNN and the
+fused member / mask / pe_idx gather.  ``ClusterMerging`` is the AFF
+downsampling layer (aff.py:122-299).
 
 ``ClusterMerging`` keeps the constructor, forward signature and parameter
 names (``weight_net``, ``norm``, ``linear``, ``global_norm``,
@@ -9,11 +14,57 @@ on the HIP kernel.
 """
 from __future__ import annotations
 
+import math
+
 import torch
 import torch.nn as nn
 
+from ..kernels.knn import knn
+from ..kernels.nbhd_index import cluster_members
 from ..kernels.weighted_features import weighted_features
-from ..utils.pos_embed import pre_table_fp32
+from ..utils.geometry import space_filling_cluster
+from ..utils.pos_embed import REL_POS_WIDTH, TABLE_WIDTH, pre_table_fp32
+
+
+def neighbourhood_index(pos, feat, h, w, cluster_size, nbhd_size, global_attention=False):
+    """Neighbourhood construction of BasicLayer.forward (reference
+    src/layers/aff.py:414-465), before its attention blocks run.
+
+    pos [b,n,2], feat [b,n,c] on an h x w canvas.  Tokens are clustered along
+    the space-filling curve into k = ceil(n / cluster_size) clusters (tokens
+    and features reordered so that each cluster is contiguous), every token's
+    nnc = min(round(nbhd_size / cluster_size), k) nearest cluster centres are
+    found by the exact KNN kernel, and one fused kernel gathers their members,
+    padding mask and relative-position table index.  Returns
+    (pos, feat, member_idx [b,n,nnc*m] int64, cluster_mask [b,n,nnc*m] int64
+    or None, pe_idx int64, global_attn, nbhd_size): the neighbourhood size is
+    rounded to a multiple of the cluster size as in the reference, and when it
+    covers every token (global attention) pe_idx is the dense [b,n,n] index.
+    The reference's training-time cache of the first stage's clustering is a
+    pure reuse of the same result and is not kept here.
+    """
+    b, n, d = pos.shape
+    c = feat.shape[2]
+    assert cluster_size > 0, "cluster_size must be positive"
+    global_attn = bool(global_attention) or nbhd_size >= n
+    k = int(math.ceil(n / float(cluster_size)))
+    nnc = min(int(round(nbhd_size / float(cluster_size))), k)
+    nbhd = cluster_size * nnc
+    if k == n:
+        cluster_mean_pos = pos
+        members = torch.arange(n, device=pos.device).reshape(1, n, 1).expand(b, -1, -1)
+        cmask = None
+    else:
+        pos, cluster_mean_pos, members, cmask, reorder = space_filling_cluster(pos, cluster_size, h, w,
+                                                                               no_reorder=False)
+        feat = feat.gather(1, reorder.expand(-1, -1, c))
+    assert members.shape[1] == k and members.shape[2] == cluster_size, "member_idx shape incorrect!"
+    nearest = knn(pos, cluster_mean_pos, nnc)
+    member_idx, cluster_mask, pe_idx = cluster_members(nearest, members, cmask, pos, with_pe=not global_attn)
+    if global_attn:
+        rel = ((pos[:, None, :, :] + REL_POS_WIDTH) - pos[:, :, None, :]).clamp(0, TABLE_WIDTH - 1)
+        pe_idx = (rel[..., 1] * TABLE_WIDTH + rel[..., 0]).long()
+    return pos, feat, member_idx, cluster_mask, pe_idx, global_attn, nbhd
 
 
 class ClusterMerging(nn.Module):

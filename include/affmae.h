@@ -127,10 +127,11 @@ typedef struct aff_nbhd_attn_args {
     void *ws; size_t ws_bytes; /* workspace: aff_nbhd_attn_workspace_bytes(args) bytes */
 } aff_nbhd_attn_args;
 
-/* Workspace the call with these arguments needs (0 when none): one byte per
- * 16-query tile when the matrix-core path runs (16-bit q/k/v, D == 32,
- * M <= 64, fp32 table in bias modes 2 and 4).  Its contents on entry do not
- * matter; calls that share it must not overlap. */
+/* Workspace the call with these arguments needs (0 when none).  The
+ * matrix-core paths take 16-bit q/k/v with D == 32 and M <= 64; with
+ * H * M <= 192 they need none, otherwise (fp32 table in bias modes 2 and 4)
+ * one byte per 32-query tile.  Its contents on entry do not matter; calls
+ * that share it must not overlap. */
 size_t aff_nbhd_attn_workspace_bytes(const aff_nbhd_attn_args *args);
 aff_status aff_nbhd_attn_fwd(const aff_nbhd_attn_args *args, aff_stream_t stream);
 
@@ -291,6 +292,34 @@ aff_status aff_msdetrpc_fwd(const void *nn_idx, int idx_is_i64, int64_t i_sb, in
                             const void *val, int dtype, int64_t v_sb, int64_t v_sn,
                             int B, int N, int M, int K, int Nval, int C,
                             void *out, int64_t o_sb, int64_t o_sn, aff_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
+ * Neighbourhood index construction of the encoder's BasicLayer.
+ *
+ * Replaces the torch gathers of BasicLayer.forward  src/layers/aff.py:452-465
+ * (member gather, padding-mask gather, relative-position table index).
+ *
+ * For token n of image b and slot j < nnc * m, with c = nearest[b, n, j / m]
+ * and i = j % m:
+ *   out_member[b, n, j] = members[b, c, i]
+ *   out_mask[b, n, j]   = cmask[b, c, i] != 0          (1 when cmask is NULL)
+ *   out_pe[b, n, j]     = trunc(rel_y * (2W + 1) + rel_x), fp32, no contraction,
+ *                         rel = clamp(pos[b, member] - (pos[b, n] - W), 0, 2W)
+ * nearest [B, N, nnc] (int32/int64, strides n_sb, n_sn, unit on the last dim),
+ * members [B, K, m] (int32/int64, strides m_sb, m_sk), cmask [B, K, m] uint8
+ * (strides c_sb, c_sk) or NULL, pos [B, N, 2] fp32 (strides p_sb, p_sn).
+ * Outputs are [B, N, nnc * m] contiguous: out_member int32/int64
+ * (out_is_i64), out_mask uint8 or NULL, out_pe int32/int64 or NULL.  A
+ * cluster id outside [0, K) or a member outside [0, N) yields member 0 and
+ * mask 0.  W = rel_width (127 in the reference).
+ * ------------------------------------------------------------------------ */
+aff_status aff_cluster_members(const void *nearest, int near_is_i64, int64_t n_sb, int64_t n_sn,
+                               const void *members, int mem_is_i64, int64_t m_sb, int64_t m_sk,
+                               const uint8_t *cmask, int64_t c_sb, int64_t c_sk,
+                               const float *pos, int64_t p_sb, int64_t p_sn,
+                               int B, int N, int K, int nnc, int m, int rel_width,
+                               void *out_member, int out_is_i64, uint8_t *out_mask,
+                               void *out_pe, int pe_is_i64, aff_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -12,7 +12,7 @@ Contents
   (``oracle_nbhd_attn``), each citing the reference lines it restates.
 * numpy restatements of the relative-position bias inputs:
   :func:`pre_table` (src/utils/pos_embed.py:9-24), :func:`pe_index`
-  (src/layers/aff.py:458-465), :func:`table_bias`
+  (src/layers/aff.py:458-465), :func:`cluster_members` (aff.py:452-465), :func:`table_bias`
   (src/layers/attention.py:72-125) and :func:`continuous_bias`.
 
 How each function is pinned (independent checks, not re-typed formulas) is
@@ -335,6 +335,33 @@ def pe_index(pos, member_idx) -> np.ndarray:
     rel = pos_m - (pos[:, :, None, :] - REL_POS_WIDTH)
     rel = np.clip(rel, 0, TABLE_WIDTH - 1)
     return (rel[..., 1] * TABLE_WIDTH + rel[..., 0]).astype(np.int64)
+
+
+def cluster_members(nearest, members, cmask=None, pos=None):
+    """Neighbourhood gathers of BasicLayer (aff.py:452-465) by explicit indexing.
+
+    member[b, n, ci * m + i] = members[b, nearest[b, n, ci], i]; a cluster id
+    outside [0, K) or a member outside [0, N) gives member 0 with mask 0.
+    mask likewise from cmask (returned only when cmask is given), pe_idx from
+    pe_index() on the gathered members (when pos is given).
+    """
+    nearest = np.asarray(nearest, dtype=np.int64)
+    members = np.asarray(members, dtype=np.int64)
+    B, N, nnc = nearest.shape
+    K, m = members.shape[1], members.shape[2]
+    cok = (nearest >= 0) & (nearest < K)
+    nc = np.where(cok, nearest, 0)
+    bi = np.arange(B)[:, None, None, None]
+    ii = np.arange(m)[None, None, None, :]
+    mem = members[bi, nc[..., None], ii]                                  # [B, N, nnc, m]
+    keep = np.broadcast_to(cok[..., None], mem.shape).copy()
+    if cmask is not None:
+        keep &= np.asarray(cmask)[bi, nc[..., None], ii] != 0
+    bad = (mem < 0) | (mem >= N) | ~cok[..., None]
+    mem = np.where(bad, 0, mem).reshape(B, N, nnc * m)
+    keep = (keep & ~bad).reshape(B, N, nnc * m)
+    pe = pe_index(pos, mem) if pos is not None else None
+    return mem, (keep.astype(np.int64) if cmask is not None else None), pe
 
 
 def table_bias(pe_idx, table) -> np.ndarray:

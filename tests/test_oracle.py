@@ -399,3 +399,54 @@ def test_msdetrpc_and_sample_closed_forms(oracle_mod):
     w1, _ = oracle_mod.deform_sample(sl, kv, nb, 1.0, 1)
     e = np.exp(-np.sqrt(np.array([1e-6, 25 + 1e-6])) + np.sqrt(1e-6))
     np.testing.assert_allclose(w1[0, 0], e / (e.sum() + 1e-8), rtol=1e-9)
+
+
+# ------------------------------------------------ BasicLayer index glue ----
+def _reference_style_members(nearest, members, cmask, pos, W=127, T=255):
+    """The reference's own torch expressions (aff.py:452-465): gather along the
+    cluster axis with an expanded index, then the rel_pos / clamp / pe_idx chain."""
+    import torch
+    nr = torch.from_numpy(nearest)
+    mb = torch.from_numpy(members)
+    b, n, nnc = nr.shape
+    m = mb.shape[2]
+    idx = nr.view(b, -1, 1).expand(-1, -1, m)
+    member_idx = mb.gather(index=idx, dim=1).reshape(b, n, nnc * m)
+    mask = torch.from_numpy(cmask).gather(index=idx, dim=1).reshape(b, n, nnc * m) if cmask is not None else None
+    p = torch.from_numpy(pos)
+    pos_ = p.gather(index=member_idx.view(b, -1, 1).expand(-1, -1, 2), dim=1).reshape(b, n, nnc * m, 2)
+    rel = (pos_ - (p.unsqueeze(2) - W)).clamp(0, T - 1)
+    pe = (rel[..., 1] * T + rel[..., 0]).long()
+    return member_idx.numpy(), None if mask is None else mask.numpy(), pe.numpy()
+
+
+def test_cluster_members_matches_reference_gathers(oracle_mod):
+    """Explicit-indexing oracle == the reference's gather/expand expressions on random
+    clusters (padding mask included), and == the closed form of the reordered case."""
+    rng = np.random.default_rng(5)
+    B, N, K, m, nnc = 2, 203, 26, 8, 5
+    members = rng.integers(0, N, (B, K, m))
+    cmask = (rng.random((B, K, m)) > 0.2).astype(np.int64)
+    pos = (rng.random((B, N, 2)) * 40).astype(np.float32)
+    nearest = np.stack([np.stack([rng.permutation(K)[:nnc] for _ in range(N)]) for _ in range(B)])
+    mo, ko, po = oracle_mod.cluster_members(nearest, members, cmask, pos)
+    mr, kr, pr = _reference_style_members(nearest, members, cmask, pos)
+    assert np.array_equal(mo, mr) and np.array_equal(ko, kr) and np.array_equal(po, pr)
+    # reordered tokens (space_filling_cluster with no_reorder=False): cluster c holds
+    # tokens c*m .. c*m+m-1, padding slots hold token 0 with mask 0
+    members = np.broadcast_to(np.where(np.arange(K * m) < N, np.arange(K * m), 0).reshape(1, K, m), (B, K, m))
+    cmask = np.broadcast_to((np.arange(K * m) < N).astype(np.int64).reshape(1, K, m), (B, K, m))
+    mo, ko, _ = oracle_mod.cluster_members(nearest, members, cmask)
+    c = np.repeat(nearest, m, axis=2)
+    i = np.tile(np.arange(m), nnc)[None, None, :]
+    tok = c * m + i
+    assert np.array_equal(mo, np.where(tok < N, tok, 0)) and np.array_equal(ko, (tok < N).astype(np.int64))
+
+
+def test_cluster_members_out_of_range(oracle_mod):
+    """Cluster ids outside [0, K) and members outside [0, N) give member 0, mask 0."""
+    members = np.array([[[0, 1], [1, 99], [2, 0]]])          # N = 2 tokens: 99 and 2 are out of range
+    nearest = np.array([[[1, -1], [7, 0]]])
+    mo, ko, _ = oracle_mod.cluster_members(nearest, members, np.ones((1, 3, 2), np.int64))
+    assert mo.tolist() == [[[1, 0, 0, 0], [0, 0, 0, 1]]]
+    assert ko.tolist() == [[[1, 0, 0, 0], [0, 0, 1, 1]]]
