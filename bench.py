@@ -321,7 +321,7 @@ def main() -> int:
         "attention": {"ms": attn_ms, "tokens_per_s": B * N / (attn_ms * 1e-3),
                       "raster_order_ms": attn_raster_ms},
         "roofline": {
-            "kernel": "nbhd_attn_tile_kernel<bf16_t, 4>",
+            "kernel": "nbhd_attn_wave_kernel<bf16_t, 4, false, true>",
             "bound": "hbm",
             "achieved": achieved / 1e9,
             "peak": HBM_PEAK / 1e9,
