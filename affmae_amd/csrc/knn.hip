@@ -347,8 +347,10 @@ __global__ __launch_bounds__(QUERY_THREADS) void knn_query_kernel(const float *_
 
 // ------------------------------------------------------- windowed kernel --
 constexpr int WIN_THREADS = 64;
-constexpr int WMAX = 640;       // window points held in LDS
+constexpr int WMAX = 640;       // window points held in LDS (queries as dense as the points)
+constexpr int WMAX_WIDE = 1024; // the same for sparser queries (M < N / 2): wider windows
 constexpr int WCMAX = 320;      // window cell-offset entries, (WX + 1) * WY
+constexpr int WCMAX_WIDE = 640; // the same for the wide window
 constexpr int WROWS = 64;       // window rows (one lane each while sizing)
 constexpr float WIN_U = 1.6f;   // window disk: radius^2 = WIN_U * the initial estimate
 constexpr int MAX_SLOT = 65536; // 16-bit candidate slots
@@ -465,14 +467,14 @@ __device__ __forceinline__ int radius_select(Visit &&visit, float U, int k, uint
     return -1;
 }
 
-template <int CAP>
+template <int CAP, int WM, int WC>
 __global__ __launch_bounds__(WIN_THREADS) void knn_win_kernel(const float4 *__restrict__ qsorted, const Segs s,
                                                               const void *ws, WsLayout L, int M, int k,
                                                               void *__restrict__ out_idx, int idx_i64,
                                                               float *__restrict__ out_d2) {
-    __shared__ float2 s_xy[WMAX + 3];  // + spare entries read (and ignored) by the 4-wide visits
-    __shared__ uint16_t s_id[WMAX];  // point indices (the windowed path takes N <= 65536)
-    __shared__ int s_wcs[WCMAX];
+    __shared__ float2 s_xy[WM + 3];  // + spare entries read (and ignored) by the 4-wide visits
+    __shared__ uint16_t s_id[WM];  // point indices (the windowed path takes N <= 65536)
+    __shared__ int s_wcs[WC];
     __shared__ int s_rb[WROWS + 1];
     __shared__ int s_gb[WROWS];
     __shared__ uint32_t s_list[(CAP / 2 + 1) * WIN_THREADS];  // CAP entries + 2 spare entries per lane
@@ -506,7 +508,7 @@ __global__ __launch_bounds__(WIN_THREADS) void knn_win_kernel(const float4 *__re
         wx0 = cx0; wx1 = cx1; wy0 = cy0; wy1 = cy1;
     }
     const int WX = wx1 - wx0 + 1, WY = wy1 - wy0 + 1;
-    bool win = WY <= WROWS && (WX + 1) * WY <= WCMAX;
+    bool win = WY <= WROWS && (WX + 1) * WY <= WC;
     if (win) {
         int gb = 0, cnt = 0;
         if (lane < WY) {
@@ -521,7 +523,7 @@ __global__ __launch_bounds__(WIN_THREADS) void knn_win_kernel(const float4 *__re
             if (lane >= o) incl += y;
         }
         const int total = __shfl(incl, 63, 64);
-        win = total <= WMAX;
+        win = total <= WM;
         if (win) {
             if (lane < WY) {
                 s_rb[lane] = incl - cnt;
@@ -667,15 +669,21 @@ extern "C" aff_status aff_knn(const float *query, int64_t q_sb, int64_t q_sm, co
     dim3 block(knn::QUERY_THREADS);
     dim3 gridd((M + knn::QUERY_THREADS - 1) / knn::QUERY_THREADS, B);
     if (windowed) {
+        // sparser queries spread a wave's 64 queries over more points: take the wider window
+        const bool wide = 2 * (int64_t)M < (int64_t)N;
+        using WinFn = void (*)(const float4 *, const grid::Segs, const void *, grid::WsLayout, int, int, void *, int,
+                               float *);
+        WinFn fn;
         if (k <= 12)
-            hipLaunchKernelGGL(knn::knn_win_kernel<16>, gridd, block, 0, st, qsorted, s, ws, L, M, k, out_idx,
-                               idx_is_i64, out_d2);
+            fn = wide ? knn::knn_win_kernel<16, knn::WMAX_WIDE, knn::WCMAX_WIDE>
+                      : knn::knn_win_kernel<16, knn::WMAX, knn::WCMAX>;
         else if (k <= 24)
-            hipLaunchKernelGGL(knn::knn_win_kernel<32>, gridd, block, 0, st, qsorted, s, ws, L, M, k, out_idx,
-                               idx_is_i64, out_d2);
+            fn = wide ? knn::knn_win_kernel<32, knn::WMAX_WIDE, knn::WCMAX_WIDE>
+                      : knn::knn_win_kernel<32, knn::WMAX, knn::WCMAX>;
         else
-            hipLaunchKernelGGL(knn::knn_win_kernel<64>, gridd, block, 0, st, qsorted, s, ws, L, M, k, out_idx,
-                               idx_is_i64, out_d2);
+            fn = wide ? knn::knn_win_kernel<64, knn::WMAX_WIDE, knn::WCMAX_WIDE>
+                      : knn::knn_win_kernel<64, knn::WMAX, knn::WCMAX>;
+        hipLaunchKernelGGL(fn, gridd, block, 0, st, qsorted, s, ws, L, M, k, out_idx, idx_is_i64, out_d2);
     } else if (k <= 64) {
         hipLaunchKernelGGL(knn::knn_query_kernel<64>, gridd, block, 0, st, query, q_sb, q_sm, s, ws, L, M, k, out_idx,
                            idx_is_i64, out_d2);
