@@ -8,10 +8,14 @@
 //   mode IDW:     w_j = (1 / (d2_j^power + 1e-10)) / (sum + 1e-12)
 //                 (inverse_distance_weighting, src/utils/geometry.py:40-53, on squared distances)
 //   out[b, q, h, :] = sum_s attn[b, q, h, s] * sum_j w_j * values[b, level_row(l, j), h, :]
-// Phase A (one lane per sample) finds the neighbours on the level's cell grid
-// (grid2d.hpp) and stages (row, attn * w) pairs in LDS; phase B gathers the
-// value rows (8 channels per lane, 16-byte loads) and reduces in fp32.  The
-// neighbour indices never go to HBM unless the caller asks for them.
+// Three launches after the coarse grid build (grid2d.hpp): cand_count_kernel
+// and cand_fill_kernel write, for every cell of a finer grid over each level,
+// the list of points that can be among the K nearest of any location in the
+// cell; deform_cand_kernel then gives each sample one lane that scans its
+// cell's list (exact (d2, row) keys), stages (row, attn * w) pairs in the
+// wave's LDS slice, and gathers the value rows (8 channels per lane, 16-byte
+// loads) in fp32.  The neighbour indices never go to HBM unless the caller
+// asks for them.
 //
 // aff_deform_sample_fwd: the same weights from given neighbour indices
 //   (fused_deformable_attention, fused_deform_attn.py:79-231, 503-571: sqrt(d2) + 1e-6;
@@ -31,27 +35,82 @@ using namespace grid;
 constexpr int THREADS = 256;
 constexpr int KMAX = 8;    // neighbours per sample
 constexpr int NB = 8;
-constexpr int WMAX = 2048;        // window points held in LDS (all levels)
-constexpr int WROWS = THREADS;    // window cell rows (all levels), one thread each while sizing
-constexpr int WCMAX = 2048;       // window cell-offset entries (all levels)
+
+// Fine-cell candidate lists.  Every (image, level) gets a second, finer grid
+// (cells of FINE x FINE per coarse cell, FPAD coarse cells of margin around
+// the coarse grid).  The list of a fine cell holds every point that can be
+// among the K nearest of ANY location inside the cell: with R = the K-th
+// smallest over the points of their largest distance to the cell rectangle,
+// each location of the cell has K points within sqrt(R), so its K nearest
+// lie within sqrt(R) of it and hence within sqrt(R) of the rectangle.  A
+// sample then scans one short contiguous list, exactly.
+constexpr int FINE = 2;          // fine cells per coarse cell side
+constexpr int FPAD = 2;          // coarse cells of margin around the coarse grid
+constexpr int CB = 256;          // fine cells per build tile (one workgroup)
+constexpr int MAX_CAND = 128;    // longest list kept; a longer one sends its samples to the coarse grid
+
+struct FineParams {
+    float x0, y0, s, inv_s;  // origin and cell side
+    int gx, gy;              // 0 x 0: no fine grid (every sample searches the coarse grid)
+    float slack;             // absolute rounding allowance of the cell rectangles
+    int pad;
+};
+
+struct Cand {
+    float x, y;
+    int row;  // row of the point in the image's level concatenation
+};
+
+// Workspace of aff_deform_fwd: the coarse grids (grid2d.hpp), then the fine
+// grids' parameters, their (begin, count) cell tables, the per-tile candidate
+// counts and the candidate pool of each batch item.
+struct DLayout {
+    WsLayout g;
+    size_t fparams, fcell, tsum, pool, total;
+    int fc_off[MAX_SEGS + 1];    // fine-cell table offset of each level (int2 entries)
+    int fcmax[MAX_SEGS];         // fine cells reserved per level
+    int tile_off[MAX_SEGS + 1];  // first build tile of each level
+    int64_t fc_per_b, pool_per_b;
+    int tt_per_b;
+};
+
+inline int pool_per_point(int K) { return 16 + 8 * K; }
+
+inline DLayout d_layout(int B, const Segs &s, int K) {
+    DLayout d{};
+    d.g = ws_layout(B, s);
+    size_t off = d.g.total;
+    d.fparams = off;
+    off = align256(off + sizeof(FineParams) * (size_t)B * s.L);
+    int fc = 0, tt = 0;
+    for (int l = 0; l < s.L; ++l) {
+        const int cm = s.cmax[l];
+        int sq = 1;
+        while (sq * sq < cm) ++sq;
+        d.fc_off[l] = fc;
+        d.fcmax[l] = FINE * FINE * (cm + 4 * FPAD * (sq + 2) + 4 * FPAD * FPAD);
+        fc += d.fcmax[l];
+        d.tile_off[l] = tt;
+        tt += (d.fcmax[l] + CB - 1) / CB;
+    }
+    d.fc_off[s.L] = fc;
+    d.tile_off[s.L] = tt;
+    d.fc_per_b = fc;
+    d.tt_per_b = tt;
+    d.fcell = off;
+    off = align256(off + sizeof(int2) * (size_t)B * fc);
+    d.tsum = off;
+    off = align256(off + sizeof(int) * (size_t)B * tt);
+    d.pool_per_b = (int64_t)pool_per_point(K) * s.npts_b + 1024;
+    d.pool = off;
+    off = align256(off + sizeof(Cand) * (size_t)B * (size_t)d.pool_per_b);
+    d.total = off;
+    return d;
+}
 
 __device__ __forceinline__ int64_t load_index(const void *p, int is_i64, int64_t i) {
     return is_i64 ? static_cast<const int64_t *>(p)[i] : int64_t(static_cast<const int32_t *>(p)[i]);
 }
-
-struct KArgs {
-    aff_deform_args a;
-    Segs segs;
-    WsLayout wl;
-    const void *ws;
-};
-
-// Order-preserving map of a float onto int (for min / max through integer LDS ops).
-__device__ __forceinline__ int ford(float f) {
-    const int i = __float_as_int(f);
-    return i ^ ((i >> 31) & 0x7fffffff);
-}
-__device__ __forceinline__ float fdeord(int i) { return __int_as_float(i ^ ((i >> 31) & 0x7fffffff)); }
 
 // keys[0 .. KT) ascending; insert `key` if it is smaller than keys[KT - 1].
 template <int KT>
@@ -64,57 +123,9 @@ __device__ __forceinline__ void topk_insert(uint64_t (&keys)[KT], uint64_t key) 
     keys[0] = c[0] ? key : keys[0];
 }
 
-// Window of one level staged in LDS: cells [wx0, wx1] x [wy0, wy1] of the
-// level's grid; wcs[(cy - wy0) * (wx1 - wx0 + 2) + (cx - wx0)] is the LDS
-// slot of the first point of cell (cx, cy).
-struct LevelWin {
-    int wx0, wy0, wx1, wy1, wcs;  // wcs: offset of this level's table in s_wcs
-};
-
-// Exact K nearest points (keys (d2, row) ascending, KT slots, the first keff
-// meaningful) of (qx, qy) among the points of one level, visiting the cells
-// meeting the disk d2 <= U from the LDS window; U grows until the keff-th key
-// lies inside the visited disk.  Returns false when the disk leaves the
-// window (the caller then searches the global grid).
-template <int KT>
-__device__ __forceinline__ bool topk_window(const GridParams &p, const LevelWin &w, const int *wcs,
-                                            const float4 *pts, float qx, float qy, float U, int keff,
-                                            uint64_t (&keys)[KT]) {
-    const float slack = query_slack(p, qx, qy);
-    for (int it = 0; it < 32; ++it) {
-#pragma unroll
-        for (int i = 0; i < KT; ++i) keys[i] = ~0ull;
-        const float r = __builtin_amdgcn_sqrtf(U) * 1.00002f + slack;
-        const int cy0 = cell_coord(qy - r, p.y0, p.inv_h, p.gy), cy1 = cell_coord(qy + r, p.y0, p.inv_h, p.gy);
-        if (cy0 < w.wy0 || cy1 > w.wy1) return false;
-        const int wxp = w.wx1 - w.wx0 + 2;
-        for (int cy = cy0; cy <= cy1; ++cy) {
-            const float rlo = p.y0 + float(cy) * p.h, rhi = rlo + p.h;
-            const float dy = fmaxf(0.f, fmaxf(rlo - qy, qy - rhi) - slack);
-            const float w2 = r * r - dy * dy;
-            if (!(w2 >= 0.f)) continue;
-            const float hw = __builtin_amdgcn_sqrtf(w2) * 1.00002f + slack;
-            const int cx0 = cell_coord(qx - hw, p.x0, p.inv_h, p.gx), cx1 = cell_coord(qx + hw, p.x0, p.inv_h, p.gx);
-            if (cx0 < w.wx0 || cx1 > w.wx1) return false;
-            const int *row = wcs + w.wcs + (cy - w.wy0) * wxp - w.wx0;
-            const int beg = row[cx0], end = row[cx1 + 1];
-            for (int t = beg; t < end; t += 2) {  // two points per step (the array has a spare entry)
-                const float4 a0 = pts[t], a1 = pts[t + 1];
-                const uint64_t k0 = make_key(dist2(a0.x, a0.y, qx, qy), __float_as_int(a0.z));
-                const uint64_t k1 = make_key(dist2(a1.x, a1.y, qx, qy), __float_as_int(a1.z));
-                topk_insert<KT>(keys, k0);
-                if (t + 1 < end) topk_insert<KT>(keys, k1);
-            }
-        }
-        const uint64_t kth = keys[keff - 1 < KT ? keff - 1 : KT - 1];
-        if (kth != ~0ull && key_d2(kth) <= U) return true;
-        U = fmaxf(U * 2.f, kth != ~0ull ? key_d2(kth) : U);
-        if (!(U < INFINITY)) return false;
-    }
-    return false;
-}
-
-// The same search over the global grid (always completes).
+// Exact K nearest points of (qx, qy) over one level's coarse grid, keys
+// (d2, row) ascending in keys[0 .. keff): the disk d2 <= U grows until the
+// keff-th key lies inside it.
 template <int KT>
 __device__ __forceinline__ void topk_global(const SegView &g, float qx, float qy, float U, int keff,
                                             uint64_t (&keys)[KT]) {
@@ -148,333 +159,392 @@ __device__ __forceinline__ void topk_global(const SegView &g, float qx, float qy
     }
 }
 
-// SPR: lanes per (b, q, h) row = next power of two >= L * P.  KT: neighbour
-// slots per sample (>= K).  A workgroup takes PASSES blocks of R = 256 / SPR
-// consecutive rows: one LDS window (the cells of every level around all of
-// its samples) serves all of them.
-constexpr int PASSES = 8;
-
-template <typename T, int SPR, int KT>
-__global__ __launch_bounds__(THREADS) void deform_fwd_kernel(const KArgs ka) {
-    using IO = ElemIO<T>;
-    constexpr int R = THREADS / SPR;             // rows per pass
-    __shared__ __align__(16) float4 s_pts[WMAX + 1];
-    __shared__ int s_wcs[WCMAX];
-    __shared__ int s_rb[WROWS + 1];              // LDS slot of each window row's first point
-    __shared__ int s_gb[WROWS];                  // its slot in the level's cell-ordered array
-    __shared__ int s_bb[AFF_DEFORM_MAX_LEVELS][4];
-    __shared__ LevelWin s_lw[AFF_DEFORM_MAX_LEVELS];
-    __shared__ int s_lrows[AFF_DEFORM_MAX_LEVELS], s_lcells[AFF_DEFORM_MAX_LEVELS];
-    __shared__ GridParams s_gp[AFF_DEFORM_MAX_LEVELS];  // level grids of image b0
-    __shared__ float s_rho[AFF_DEFORM_MAX_LEVELS];      // their mean point densities
-    __shared__ int s_meta[4];                    // rows, cell entries, -, window ok
-    __shared__ int s_wsum[THREADS / 64];
-    __shared__ int s_row[R][SPR * KT];
-    __shared__ float s_w[R][SPR * KT];
-
-    const aff_deform_args &a = ka.a;
-    const int tid = threadIdx.x;
-    const int r = tid / SPR, t = tid % SPR;
-    const int S = a.L * a.P, K = a.K, L = a.L;
-    const int64_t total = (int64_t)a.B * a.Nq * a.H;
-    const int64_t rowA = (int64_t)xcd_swizzle(blockIdx.x, gridDim.x) * R * PASSES;
-    const int b0 = int(rowA / ((int64_t)a.Nq * a.H));  // the window's image: that of the first row
-    const int l = t < S ? t / a.P : 0;                 // level of this lane's sample (every pass)
-
-    // ---- this lane's sample in pass ps: location and attention weight
-    auto load_sample = [&](int ps, float &sx, float &sy, float &aw, int &bs) {
-        const int64_t row = rowA + ps * R + r;
-        sx = sy = aw = 0.f;
-        bs = -1;
-        if (row < total && t < S) {
-            const uint32_t rw = uint32_t(row);  // the host keeps B * Nq * H below 2^31
-            const int h = int(rw % uint32_t(a.H));
-            const uint32_t bq = rw / uint32_t(a.H);
-            const int q = int(bq % uint32_t(a.Nq)), b = int(bq / uint32_t(a.Nq));
-            const float qx = a.query_pos[(int64_t)b * a.qp_sb + (int64_t)q * a.qp_sn];
-            const float qy = a.query_pos[(int64_t)b * a.qp_sb + (int64_t)q * a.qp_sn + 1];
-            const int64_t ob = (int64_t)b * a.off_sb + (int64_t)q * a.off_sn + (int64_t)h * a.off_sh + (int64_t)t * 2;
-            sx = qx + load_any(a.offsets, a.off_dtype, ob);
-            sy = qy + load_any(a.offsets, a.off_dtype, ob + 1);
-            aw = load_any(a.attn, a.attn_dtype, (int64_t)b * a.at_sb + (int64_t)q * a.at_sn + (int64_t)h * a.at_sh + t);
-            bs = b;
+// ------------------------------------------------------ candidate lists --
+// Fine grid of one level: the coarse grid's box widened by FPAD coarse cells,
+// cells of side h / FINE, widened (x 1.0625 steps) until at most fcmax cells.
+__device__ __forceinline__ FineParams fine_params(const GridParams &p, int n, int fcmax) {
+    FineParams f{};
+    const float pad = float(FPAD) * p.h;
+    const float wd = float(p.gx) * p.h + 2.f * pad, ht = float(p.gy) * p.h + 2.f * pad;
+    f.x0 = p.x0 - pad;
+    f.y0 = p.y0 - pad;
+    float s = p.h / float(FINE);
+    int gx = 0, gy = 0;
+    if (n > 0 && s > 0.f && wd < INFINITY && ht < INFINITY && f.x0 > -INFINITY && f.y0 > -INFINITY &&
+        wd / s < 1e6f && ht / s < 1e6f) {
+        for (int it = 0; it < 256; ++it) {
+            gx = int(wd / s) + 1;
+            gy = int(ht / s) + 1;
+            if ((int64_t)gx * gy <= fcmax) break;
+            s *= 1.0625f;
+            gx = gy = 0;
         }
+    }
+    f.s = s;
+    f.inv_s = 1.f / s;
+    f.gx = gx;
+    f.gy = gy;
+    f.slack = 1e-5f * (fabsf(f.x0) + fabsf(f.y0) + wd + ht) + 1e-30f;
+    return f;
+}
+
+struct Rect {
+    float x0, y0, x1, y1;
+};
+
+// The count and fill passes must agree on every list bit for bit: the
+// geometry below is evaluated without contraction in both.
+__device__ __forceinline__ Rect fine_rect(const FineParams &f, int c) {
+#pragma clang fp contract(off)
+    const int cy = c / f.gx, cx = c - cy * f.gx;
+    Rect r;
+    r.x0 = f.x0 + float(cx) * f.s - f.slack;
+    r.x1 = f.x0 + float(cx + 1) * f.s + f.slack;
+    r.y0 = f.y0 + float(cy) * f.s - f.slack;
+    r.y1 = f.y0 + float(cy + 1) * f.s + f.slack;
+    return r;
+}
+
+// R of one fine cell: the keff-th smallest largest-distance^2 from a point to
+// the rectangle, over the points of the coarse rings around the rectangle's
+// centre (at least the 3 x 3 block; any keff points give a valid bound, the
+// nearest ones a tight one).
+template <int KT>
+__device__ __forceinline__ float cell_bound(const SegView &g, const Rect &rc, int keff) {
+#pragma clang fp contract(off)
+    const GridParams &p = g.p;
+    float top[KT];
+#pragma unroll
+    for (int i = 0; i < KT; ++i) top[i] = INFINITY;
+    int found = 0;
+    const int ccx = cell_coord(0.5f * (rc.x0 + rc.x1), p.x0, p.inv_h, p.gx);
+    const int ccy = cell_coord(0.5f * (rc.y0 + rc.y1), p.y0, p.inv_h, p.gy);
+    auto visit = [&](int cy, int cx0, int cx1) {
+        const int beg = g.cs[cy * p.gx + cx0], end = g.cs[cy * p.gx + cx1 + 1];
+        for (int t = beg; t < end; ++t) {
+            const float4 pt = g.P[t];
+            const float mx = fmaxf(fabsf(pt.x - rc.x0), fabsf(pt.x - rc.x1));
+            const float my = fmaxf(fabsf(pt.y - rc.y0), fabsf(pt.y - rc.y1));
+            float v = mx * mx + my * my;
+#pragma unroll
+            for (int i = 0; i < KT; ++i) {
+                const float lo = fminf(top[i], v);
+                v = fmaxf(top[i], v);
+                top[i] = lo;
+            }
+        }
+        found += end - beg;
     };
-    // ---- bounding box of this lane's samples over all passes (image b0)
-    int bmin = INT_MAX, bmaxx = INT_MIN, bminy = INT_MAX, bmaxy = INT_MIN;
-#pragma unroll 1
-    for (int ps = 0; ps < PASSES; ++ps) {
-        float sx, sy, aw;
-        int bs;
-        load_sample(ps, sx, sy, aw, bs);
-        if (bs == b0) {
-            bmin = min(bmin, ford(sx));
-            bmaxx = max(bmaxx, ford(sx));
-            bminy = min(bminy, ford(sy));
-            bmaxy = max(bmaxy, ford(sy));
+    for (int rad = 0;; ++rad) {
+        const int ax0 = ccx - rad, ax1 = ccx + rad, ay0 = ccy - rad, ay1 = ccy + rad;
+        const int ylo = max(ay0, 0), yhi = min(ay1, p.gy - 1);
+        for (int cy = ylo; cy <= yhi; ++cy) {
+            if (cy == ay0 || cy == ay1) {
+                visit(cy, max(ax0, 0), min(ax1, p.gx - 1));
+            } else {
+                if (ax0 >= 0) visit(cy, ax0, ax0);
+                if (ax1 < p.gx) visit(cy, ax1, ax1);
+            }
         }
+        const bool full = ax0 <= 0 && ay0 <= 0 && ax1 >= p.gx - 1 && ay1 >= p.gy - 1;
+        if ((found >= keff && rad >= 1) || full) break;
     }
-    if (tid < AFF_DEFORM_MAX_LEVELS * 4) (&s_bb[0][0])[tid] = (tid & 1) ? INT_MIN : INT_MAX;
-    __syncthreads();
-    // ---- per-level bounding box of the workgroup's samples (image b0)
-    if (bmin != INT_MAX) {
-        atomicMin(&s_bb[l][0], bmin);
-        atomicMax(&s_bb[l][1], bmaxx);
-        atomicMin(&s_bb[l][2], bminy);
-        atomicMax(&s_bb[l][3], bmaxy);
-    }
-    __syncthreads();
-
-    // ---- window rectangles (thread lv per level): the box widened by 2 x the
-    // radius holding K + 4 points at the level's mean density; a lane whose search
-    // disk still leaves the window searches the global grid instead
-    if (tid < L) {
-        const int lv = tid;
-        const SegView g = seg_view(ka.ws, ka.wl, ka.segs, b0, lv);
-        const GridParams &p = g.p;
-        LevelWin w{0, 0, -1, -1, 0};
-        const float area = float(p.gx) * float(p.gy) * p.h * p.h;
-        const float rho = float(g.n) / fmaxf(area, 1e-30f);
-        s_gp[lv] = p;
-        s_rho[lv] = rho;
-        if (s_bb[lv][0] != INT_MAX && g.n > 0) {
-            const float m = 2.f * sqrtf(float(K + 4) / (3.14159265f * rho));
-            w.wx0 = cell_coord(fdeord(s_bb[lv][0]) - m, p.x0, p.inv_h, p.gx);
-            w.wx1 = cell_coord(fdeord(s_bb[lv][1]) + m, p.x0, p.inv_h, p.gx);
-            w.wy0 = cell_coord(fdeord(s_bb[lv][2]) - m, p.y0, p.inv_h, p.gy);
-            w.wy1 = cell_coord(fdeord(s_bb[lv][3]) + m, p.y0, p.inv_h, p.gy);
-        }
-        s_lw[lv] = w;
-        s_lrows[lv] = w.wy1 - w.wy0 + 1;
-        s_lcells[lv] = (w.wx1 - w.wx0 + 2) * (w.wy1 - w.wy0 + 1);
-    }
-    __syncthreads();
-    if (tid == 0) {
-        int rows = 0, cells = 0;
-        for (int lv = 0; lv < L; ++lv) {
-            s_lw[lv].wcs = cells;
-            rows += s_lrows[lv];
-            cells += s_lcells[lv];
-        }
-        s_meta[0] = rows;
-        s_meta[1] = cells;
-        s_meta[3] = (rows <= WROWS && cells <= WCMAX) ? 1 : 0;
-    }
-    __syncthreads();
-    bool win = s_meta[3] != 0;
-    if (win) {
-        // window row `tid`: its level, its cell range in the level's cell-ordered array
-        const int nrows = s_meta[0];
-        int cnt = 0, gb = 0;
-        if (tid < nrows) {
-            int lv = 0, base = 0;
-            while (tid >= base + s_lrows[lv]) base += s_lrows[lv++];
-            const LevelWin w = s_lw[lv];
-            const SegView g = seg_view(ka.ws, ka.wl, ka.segs, b0, lv);
-            const int *crow = g.cs + (w.wy0 + tid - base) * g.p.gx;
-            gb = crow[w.wx0];
-            cnt = crow[w.wx1 + 1] - gb;
-        }
-        // block exclusive scan of the row counts
-        const int lane = tid & 63, wid = tid >> 6;
-        int incl = cnt;
+    float R = top[0];
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(incl, o, 64);
-            if (lane >= o) incl += y;
+    for (int i = 1; i < KT; ++i)
+        if (i < keff) R = top[i];
+    return R * 1.0001f + 1e-30f;
+}
+
+// Calls f(point) for every point of the level whose distance^2 to the
+// rectangle is at most R, in the coarse grid's cell order.
+template <typename F>
+__device__ __forceinline__ void visit_cands(const SegView &g, const Rect &rc, float R, F &&f) {
+#pragma clang fp contract(off)
+    const GridParams &p = g.p;
+    const float rr = sqrtf(R) * 1.00002f + query_slack(p, rc.x0, rc.y0);
+    const int cy0 = cell_coord(rc.y0 - rr, p.y0, p.inv_h, p.gy), cy1 = cell_coord(rc.y1 + rr, p.y0, p.inv_h, p.gy);
+    const int cx0 = cell_coord(rc.x0 - rr, p.x0, p.inv_h, p.gx), cx1 = cell_coord(rc.x1 + rr, p.x0, p.inv_h, p.gx);
+    for (int cy = cy0; cy <= cy1; ++cy) {
+        const int beg = g.cs[cy * p.gx + cx0], end = g.cs[cy * p.gx + cx1 + 1];
+        for (int t = beg; t < end; ++t) {
+            const float4 pt = g.P[t];
+            const float dx = fmaxf(0.f, fmaxf(rc.x0 - pt.x, pt.x - rc.x1));
+            const float dy = fmaxf(0.f, fmaxf(rc.y0 - pt.y, pt.y - rc.y1));
+            if (dx * dx + dy * dy <= R) f(pt);
         }
-        if (lane == 63) s_wsum[wid] = incl;
-        __syncthreads();
-        int off = 0;
-        for (int i = 0; i < wid; ++i) off += s_wsum[i];
-        const int total_pts = s_wsum[0] + s_wsum[1] + s_wsum[2] + s_wsum[3];
-        if (tid < nrows) {
-            s_rb[tid] = off + incl - cnt;
-            s_gb[tid] = gb;
-        }
-        if (tid == 0) s_rb[nrows] = total_pts;
-        win = total_pts <= WMAX;
-        __syncthreads();
-        if (win) {
-            // cell-offset tables, then the points (x, y, row in the image's level
-            // concatenation, as the global grid stores them)
-            const int ncells = s_meta[1];
-            for (int e = tid; e < ncells; e += THREADS) {
-                int lv = 0, rbase = 0;
-                while (lv + 1 < L && e >= s_lw[lv + 1].wcs) rbase += s_lrows[lv++];
-                const LevelWin &w = s_lw[lv];
-                const int wxp = w.wx1 - w.wx0 + 2, el = e - w.wcs;
-                const int rr = el / wxp, c = el - rr * wxp;
-                const SegView g = seg_view(ka.ws, ka.wl, ka.segs, b0, lv);
-                s_wcs[e] = s_rb[rbase + rr] + g.cs[(w.wy0 + rr) * g.p.gx + w.wx0 + c] - s_gb[rbase + rr];
-            }
-            for (int e = tid; e < total_pts; e += THREADS) {
-                int lo = 0, hi = nrows - 1;  // last row with s_rb[row] <= e
-                while (lo < hi) {
-                    const int mid = (lo + hi + 1) >> 1;
-                    if (s_rb[mid] <= e) lo = mid; else hi = mid - 1;
-                }
-                int lv = 0, base = 0;
-                while (lo >= base + s_lrows[lv]) base += s_lrows[lv++];
-                const SegView g = seg_view(ka.ws, ka.wl, ka.segs, b0, lv);
-                s_pts[e] = g.P[s_gb[lo] + (e - s_rb[lo])];
-            }
-            if (tid == 0) s_pts[total_pts] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-        __syncthreads();
     }
+}
+
+struct BArgs {
+    Segs segs;
+    WsLayout wl;
+    const void *ws;
+    FineParams *fp;  // [B * L]
+    int2 *fcell;     // [B][fc_per_b]: (R bits, count) after the count pass, (begin, count) after the fill
+    int *tsum;       // [B][tt_per_b]
+    Cand *pool;      // [B][pool_per_b]
+    int fc_off[MAX_SEGS + 1], fcmax[MAX_SEGS], tile_off[MAX_SEGS + 1];
+    int64_t fc_per_b, pool_per_b;
+    int tt_per_b, K;
+};
+
+// Exclusive prefix of v over the 256 threads; *total gets the sum.
+__device__ __forceinline__ int block_scan(int v, int *s_w, int *total) {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    int incl = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += y;
+    }
+    if (lane == 63) s_w[wid] = incl;
+    __syncthreads();
+    int off = 0;
+    for (int i = 0; i < wid; ++i) off += s_w[i];
+    *total = s_w[0] + s_w[1] + s_w[2] + s_w[3];
+    __syncthreads();
+    return off + incl - v;
+}
+
+__device__ __forceinline__ void tile_of(const BArgs &ba, int &b, int &l, int &t, int &gt) {
+    b = blockIdx.x / ba.tt_per_b;
+    gt = blockIdx.x - b * ba.tt_per_b;
+    l = 0;
+    while (l + 1 < ba.segs.L && gt >= ba.tile_off[l + 1]) ++l;
+    t = gt - ba.tile_off[l];
+}
+
+// Pass 1: one lane per fine cell: R and the list length.
+template <int KT>
+__global__ __launch_bounds__(CB) void cand_count_kernel(const BArgs ba) {
+    __shared__ int s_w[4];
+    int b, l, t, gt;
+    tile_of(ba, b, l, t, gt);
+    const SegView g = seg_view(ba.ws, ba.wl, ba.segs, b, l);
+    const FineParams f = fine_params(g.p, g.n, ba.fcmax[l]);
+    if (t == 0 && threadIdx.x == 0) ba.fp[b * ba.segs.L + l] = f;
+    const int c = t * CB + threadIdx.x;
+    const bool valid = c < f.gx * f.gy;
+    int cnt = 0;
+    float R = 0.f;
+    if (valid && g.n > 0) {
+        const Rect rc = fine_rect(f, c);
+        R = cell_bound<KT>(g, rc, min(ba.K, g.n));
+        visit_cands(g, rc, R, [&](const float4 &) { ++cnt; });
+    }
+    if (cnt > MAX_CAND) cnt = -1;
+    if (valid) ba.fcell[b * ba.fc_per_b + ba.fc_off[l] + c] = make_int2(__float_as_int(R), cnt);
+    int tot;
+    block_scan(max(cnt, 0), s_w, &tot);
+    if (threadIdx.x == 0) ba.tsum[b * ba.tt_per_b + gt] = tot;
+}
+
+// Pass 2: list offsets (the counts of all earlier tiles of the image, then
+// this tile's prefix) and the entries.  Lists that do not fit the pool get
+// count -1: their samples search the coarse grid.
+template <int KT>
+__global__ __launch_bounds__(CB) void cand_fill_kernel(const BArgs ba) {
+    __shared__ int s_w[4];
+    int b, l, t, gt;
+    tile_of(ba, b, l, t, gt);
+    const FineParams f = ba.fp[b * ba.segs.L + l];
+    const int c = t * CB + threadIdx.x;
+    if (t * CB >= f.gx * f.gy) return;  // whole tile outside the grid
+    const bool valid = c < f.gx * f.gy;
+    int2 e = valid ? ba.fcell[b * ba.fc_per_b + ba.fc_off[l] + c] : make_int2(0, 0);
+    int before = 0;
+    for (int i = threadIdx.x; i < gt; i += CB) before += ba.tsum[b * ba.tt_per_b + i];
+    int base;
+    block_scan(before, s_w, &base);
+    int tot;
+    const int pre = block_scan(max(e.y, 0), s_w, &tot);
+    const int64_t begin = (int64_t)base + pre;
+    if (!valid) return;
+    int cnt = e.y;
+    if (cnt > 0 && begin + cnt > ba.pool_per_b) cnt = -1;
+    ba.fcell[b * ba.fc_per_b + ba.fc_off[l] + c] = make_int2(int(begin), cnt);
+    if (cnt > 0) {
+        const SegView g = seg_view(ba.ws, ba.wl, ba.segs, b, l);
+        const Rect rc = fine_rect(f, c);
+        Cand *out = ba.pool + b * ba.pool_per_b + begin;
+        int k = 0;
+        visit_cands(g, rc, __int_as_float(e.x), [&](const float4 &pt) {
+            if (k < cnt) out[k] = Cand{pt.x, pt.y, __float_as_int(pt.z)};
+            ++k;
+        });
+    }
+}
+
+// --------------------------------------------------------- main kernel --
+struct CArgs {
+    aff_deform_args a;
+    Segs segs;
+    WsLayout wl;
+    const void *ws;
+    const FineParams *fp;
+    const int2 *fcell;
+    const Cand *pool;
+    int fc_off[MAX_SEGS + 1];
+    int64_t fc_per_b, pool_per_b;
+    int pl_log2;  // lanes per row = 2^pl_log2 >= P
+};
+
+// One wave = RW = 64 / PL consecutive (b, q, h) rows.  Search: lane (r, p)
+// takes sample (l, p) of row r for every level l, scans its fine cell's list
+// (or the coarse grid outside the fine grid) and stages (row, attn * w) of its
+// K neighbours in the wave's LDS slice.  Gather: lane (r, chunk) sums the
+// row's L * P * K value rows over 8 channels (16-byte loads) in fp32.  Waves
+// share nothing; the workgroup only batches them.
+template <typename T, int KT>
+__global__ __launch_bounds__(THREADS) void deform_cand_kernel(const CArgs ka) {
+    using IO = ElemIO<T>;
+    extern __shared__ int2 s_pair[];
+    const aff_deform_args &a = ka.a;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nwv = blockDim.x >> 6;
+    const int PL = 1 << ka.pl_log2, RW = 64 >> ka.pl_log2;
+    const int S = a.L * a.P, K = a.K, SK = S * K;
+    int2 *pr = s_pair + wv * RW * SK;
+    const int64_t total = (int64_t)a.B * a.Nq * a.H;
+    const int64_t row0 = ((int64_t)xcd_swizzle(blockIdx.x, gridDim.x) * nwv + wv) * RW;
     const float pw = *a.power;
-    float nsx, nsy, naw;  // the next pass's sample, loaded one pass ahead
-    int nbs;
-    load_sample(0, nsx, nsy, naw, nbs);
 
-#pragma unroll 1
-    for (int ps = 0; ps < PASSES; ++ps) {
-    const float sx = nsx, sy = nsy, aw = naw;
-    if (ps + 1 < PASSES) load_sample(ps + 1, nsx, nsy, naw, nbs);
-    const int64_t row = rowA + ps * R + r;
-    const bool active = row < total;
-    const uint32_t rw = active ? uint32_t(row) : 0u;
-    const int h = int(rw % uint32_t(a.H));
-    const uint32_t bq = rw / uint32_t(a.H);
-    const int q = int(bq % uint32_t(a.Nq)), b = int(bq / uint32_t(a.Nq));
-    const bool samp = active && t < S;
-
-    // ---- phase A: one lane per sample; pairs of sample t occupy slots [t * K, t * K + K)
-    for (int j = 0; j < KT; ++j) {
-        s_row[r][t * KT + j] = -1;
-        s_w[r][t * KT + j] = 0.f;
+    {
+        const int r = lane >> ka.pl_log2, p = lane & (PL - 1);
+        const int64_t row = row0 + r;
+        const bool act = row < total && p < a.P;
+        const uint32_t rw = act ? uint32_t(row) : 0u;  // the host keeps B * Nq * H below 2^31
+        const int h = int(rw % uint32_t(a.H));
+        const uint32_t bq = rw / uint32_t(a.H);
+        const int q = int(bq % uint32_t(a.Nq)), b = int(bq / uint32_t(a.Nq));
+        float qx = 0.f, qy = 0.f;
+        if (act) {
+            qx = a.query_pos[(int64_t)b * a.qp_sb + (int64_t)q * a.qp_sn];
+            qy = a.query_pos[(int64_t)b * a.qp_sb + (int64_t)q * a.qp_sn + 1];
+        }
+        const int64_t ob = (int64_t)b * a.off_sb + (int64_t)q * a.off_sn + (int64_t)h * a.off_sh;
+        const int64_t ab = (int64_t)b * a.at_sb + (int64_t)q * a.at_sn + (int64_t)h * a.at_sh;
+        for (int l = 0; l < a.L; ++l) {
+            const int s = l * a.P + p;
+            const int lstart = ka.segs.start[l];
+            const int keff = min(K, ka.segs.start[l + 1] - lstart);
+            uint64_t keys[KT];
+#pragma unroll
+            for (int j = 0; j < KT; ++j) keys[j] = ~0ull;
+            float aw = 0.f;
+            if (act && keff > 0) {
+                const float sx = qx + load_any(a.offsets, a.off_dtype, ob + s * 2);
+                const float sy = qy + load_any(a.offsets, a.off_dtype, ob + s * 2 + 1);
+                aw = load_any(a.attn, a.attn_dtype, ab + s);
+                const FineParams f = ka.fp[b * a.L + l];
+                int beg = 0, cnt = -1;
+                {
+#pragma clang fp contract(off)
+                    const float fx = floorf(__fmul_rn(__fsub_rn(sx, f.x0), f.inv_s));
+                    const float fy = floorf(__fmul_rn(__fsub_rn(sy, f.y0), f.inv_s));
+                    if (fx >= 0.f && fx < float(f.gx) && fy >= 0.f && fy < float(f.gy)) {
+                        const int2 e = ka.fcell[b * ka.fc_per_b + ka.fc_off[l] + int(fy) * f.gx + int(fx)];
+                        beg = e.x;
+                        cnt = e.y;
+                    }
+                }
+                if (cnt > 0) {
+                    const Cand *cp = ka.pool + b * ka.pool_per_b + beg;
+                    for (int i = 0; i < cnt; i += 4) {
+                        Cand c4[4];
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) c4[u] = cp[min(i + u, cnt - 1)];
+#pragma unroll
+                        for (int u = 0; u < 4; ++u)
+                            if (i + u < cnt) topk_insert<KT>(keys, make_key(dist2(c4[u].x, c4[u].y, sx, sy), c4[u].row));
+                    }
+                } else {
+                    const SegView g = seg_view(ka.ws, ka.wl, ka.segs, b, l);
+                    const float area = float(g.p.gx) * float(g.p.gy) * g.p.h * g.p.h;
+                    const float rho = float(g.n) / fmaxf(area, 1e-30f);
+                    const float U0 = keff >= g.n ? INFINITY : fmaxf(float(keff + 4) / (3.14159265f * rho), 1e-30f);
+                    topk_global<KT>(g, sx, sy, U0, keff, keys);
+                }
+            }
+            if (act) {
+                float wj[KT];
+                float wsum = 0.f;
+                if (a.mode == AFF_DEFORM_SHEPARD) {
+                    const float pp = fmaxf(pw, 1e-6f);
+                    float lg[KT], mx = -INFINITY;
+#pragma unroll
+                    for (int j = 0; j < KT; ++j) {
+                        lg[j] = j < keff ? -pp * (sqrtf(key_d2(keys[j])) + 1e-6f) : -INFINITY;
+                        mx = fmaxf(mx, lg[j]);
+                    }
+#pragma unroll
+                    for (int j = 0; j < KT; ++j) {
+                        wj[j] = j < keff ? __expf(lg[j] - mx) : 0.f;
+                        wsum += wj[j];
+                    }
+                    wsum += 1e-8f;
+                } else {
+#pragma unroll
+                    for (int j = 0; j < KT; ++j) {
+                        wj[j] = j < keff ? 1.f / (__powf(key_d2(keys[j]), pw) + 1e-10f) : 0.f;
+                        wsum += wj[j];
+                    }
+                    wsum += 1e-12f;
+                }
+                const float inv = 1.f / wsum;
+                int2 *dst = pr + r * SK + s * K;
+                const int64_t kb = (row * S + s) * K;  // [B, Nq, H, L, P, K]
+#pragma unroll
+                for (int j = 0; j < KT; ++j) {
+                    if (j < K) {
+                        const bool ok = j < keff;
+                        dst[j] = make_int2(ok ? key_index(keys[j]) : -1, __float_as_int(ok ? aw * wj[j] * inv : 0.f));
+                        if (a.knn_idx) a.knn_idx[kb + j] = ok ? key_index(keys[j]) - lstart : -1;
+                        if (a.knn_d2) a.knn_d2[kb + j] = ok ? key_d2(keys[j]) : INFINITY;
+                    }
+                }
+            }
+        }
     }
-    __syncthreads();
-    if (samp) {
-        const int nl = ka.segs.start[l + 1] - ka.segs.start[l];
-        const int keff = min(K, nl);
-        uint64_t keys[KT];
-#pragma unroll
-        for (int j = 0; j < KT; ++j) keys[j] = ~0ull;
-        if (keff > 0) {
-            // initial radius^2: the disk holding keff + 4 points at the level's mean density
-            bool done = false;
-            if (win && b == b0 && keff < nl) {
-                const float U0 = fmaxf(float(keff + 4) / (3.14159265f * s_rho[l]), 1e-30f);
-                done = topk_window<KT>(s_gp[l], s_lw[l], s_wcs, s_pts, sx, sy, U0, keff, keys);
-            }
-            if (!done) {
-                const SegView g = seg_view(ka.ws, ka.wl, ka.segs, b, l);
-                const float area = float(g.p.gx) * float(g.p.gy) * g.p.h * g.p.h;
-                const float rho = float(g.n) / fmaxf(area, 1e-30f);
-                const float U0 = keff >= g.n ? INFINITY : fmaxf(float(keff + 4) / (3.14159265f * rho), 1e-30f);
-                topk_global<KT>(g, sx, sy, U0, keff, keys);
-            }
-        }
-        float wj[KT];
-        float wsum = 0.f;
-        if (a.mode == AFF_DEFORM_SHEPARD) {
-            const float p = fmaxf(pw, 1e-6f);
-            float lg[KT], mx = -INFINITY;
-#pragma unroll
-            for (int j = 0; j < KT; ++j) {
-                lg[j] = j < keff ? -p * (sqrtf(key_d2(keys[j])) + 1e-6f) : -INFINITY;
-                mx = fmaxf(mx, lg[j]);
-            }
-#pragma unroll
-            for (int j = 0; j < KT; ++j) {
-                wj[j] = j < keff ? __expf(lg[j] - mx) : 0.f;
-                wsum += wj[j];
-            }
-            wsum += 1e-8f;
-        } else {
-#pragma unroll
-            for (int j = 0; j < KT; ++j) {
-                wj[j] = j < keff ? 1.f / (__powf(key_d2(keys[j]), pw) + 1e-10f) : 0.f;
-                wsum += wj[j];
-            }
-            wsum += 1e-12f;
-        }
-        const float inv = 1.f / wsum;
-        const int64_t kb = ((row * a.L * a.P) + t) * K;   // [B, Nq, H, L, P, K]
-        const int lstart = ka.segs.start[l];
-#pragma unroll
-        for (int j = 0; j < KT; ++j) {
-            if (j < keff) {
-                s_row[r][t * K + j] = key_index(keys[j]);
-                s_w[r][t * K + j] = aw * wj[j] * inv;
-            }
-            if (j < K) {
-                if (a.knn_idx) a.knn_idx[kb + j] = j < keff ? key_index(keys[j]) - lstart : -1;
-                if (a.knn_d2) a.knn_d2[kb + j] = j < keff ? key_d2(keys[j]) : INFINITY;
-            }
-        }
-    }
-    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // ---- phase B: value gather.  Lane t of a row: channel chunk cc = t % CG,
-    // pair subset sg = t / CG (pairs sg, sg + NSG, ...), then the subsets are
-    // summed across lanes.  Pairs of sample s sit at [s * K, s * K + K) within
-    // the row's staging (K <= KT).
-    const int C = a.C, CG = C / 8;
-    const int npair = S * K;
-    const T *V = static_cast<const T *>(a.values) + (int64_t)b * a.v_sb + (int64_t)h * a.v_sh;
-    T *O = static_cast<T *>(a.out) + (int64_t)b * a.o_sb + (int64_t)q * a.o_sn + (int64_t)h * a.o_sh;
-    if (SPR >= CG) {
-        const int NSG = SPR / CG;
-        const int cc = t % CG, sg = t / CG;
+    const int CG = a.C / 8;
+    for (int it = lane; it < RW * CG; it += 64) {
+        const int rr = it / CG, cc = it - rr * CG;
+        const int64_t row = row0 + rr;
+        if (row >= total) break;  // rows ascend with it
+        const uint32_t rw = uint32_t(row);
+        const int h = int(rw % uint32_t(a.H));
+        const uint32_t bq = rw / uint32_t(a.H);
+        const int q = int(bq % uint32_t(a.Nq)), b = int(bq / uint32_t(a.Nq));
+        const T *V = static_cast<const T *>(a.values) + (int64_t)b * a.v_sb + (int64_t)h * a.v_sh + cc * 8;
+        T *O = static_cast<T *>(a.out) + (int64_t)b * a.o_sb + (int64_t)q * a.o_sn + (int64_t)h * a.o_sh + cc * 8;
+        const int2 *pp = pr + rr * SK;
         float acc[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-        if (active) {
-            for (int j0 = sg; j0 < npair; j0 += NSG * NB) {
-                typename IO::raw8 fr[NB];
-                float wv[NB];
+        for (int j0 = 0; j0 < SK; j0 += NB) {
+            typename IO::raw8 fr[NB];
+            float wv[NB];
 #pragma unroll
-                for (int u = 0; u < NB; ++u) {
-                    const int j = j0 + u * NSG;
-                    const int rr = j < npair ? s_row[r][j] : -1;
-                    wv[u] = rr >= 0 ? s_w[r][j] : 0.f;
-                    fr[u] = IO::load_raw(V + (int64_t)(rr >= 0 ? rr : 0) * a.v_sn + cc * 8);
-                }
+            for (int u = 0; u < NB; ++u) {
+                const int j = j0 + u;
+                const int2 e = j < SK ? pp[j] : make_int2(-1, 0);
+                wv[u] = e.x >= 0 ? __int_as_float(e.y) : 0.f;
+                fr[u] = IO::load_raw(V + (int64_t)(e.x >= 0 ? e.x : 0) * a.v_sn);
+            }
 #pragma unroll
-                for (int u = 0; u < NB; ++u) {
-                    float fv[8];
-                    IO::cvt(fr[u], fv);
+            for (int u = 0; u < NB; ++u) {
+                float fv[8];
+                IO::cvt(fr[u], fv);
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) acc[e] += wv[u] * fv[e];
-                }
+                for (int e = 0; e < 8; ++e) acc[e] += wv[u] * fv[e];
             }
         }
-        // sum the NSG subsets: lanes cc, cc + CG, ... of the row
-        for (int o = CG; o < SPR; o <<= 1)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], o, 64);
-        if (active && sg == 0) IO::store8(O + cc * 8, acc);
-    } else if (active) {
-        for (int cc = t; cc < CG; cc += SPR) {
-            float acc[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-            for (int j0 = 0; j0 < npair; j0 += NB) {
-                typename IO::raw8 fr[NB];
-                float wv[NB];
-#pragma unroll
-                for (int u = 0; u < NB; ++u) {
-                    const int j = j0 + u;
-                    const int rr = j < npair ? s_row[r][j] : -1;
-                    wv[u] = rr >= 0 ? s_w[r][j] : 0.f;
-                    fr[u] = IO::load_raw(V + (int64_t)(rr >= 0 ? rr : 0) * a.v_sn + cc * 8);
-                }
-#pragma unroll
-                for (int u = 0; u < NB; ++u) {
-                    float fv[8];
-                    IO::cvt(fr[u], fv);
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) acc[e] += wv[u] * fv[e];
-                }
-            }
-            IO::store8(O + cc * 8, acc);
-        }
+        IO::store8(O, acc);
     }
-    __syncthreads();  // the next pass rewrites s_row / s_w
-    }  // passes
 }
 
 // ------------------------------------------------ given neighbour indices --
@@ -652,25 +722,57 @@ inline int lanes_for(int C) {
 inline bool a16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 template <typename T, int KT>
-aff_status launch_deform_k(const KArgs &ka, int spr, hipStream_t s) {
-    const int64_t rows = (int64_t)ka.a.B * ka.a.Nq * ka.a.H;
-    const int64_t per_block = (THREADS / spr) * PASSES;
-    const int64_t blocks = (rows + per_block - 1) / per_block;
-    switch (spr) {
-#define DF_CASE(S) case S: hipLaunchKernelGGL((deform_fwd_kernel<T, S, KT>), dim3((unsigned)blocks), dim3(THREADS), 0, s, ka); break;
-        DF_CASE(1) DF_CASE(2) DF_CASE(4) DF_CASE(8) DF_CASE(16) DF_CASE(32)
-#undef DF_CASE
-        default: return fail(AFF_ERR_UNSUPPORTED, "aff_deform_fwd: L*P=%d exceeds 32", spr);
+aff_status launch_deform_k(const aff_deform_args &a, const Segs &segs, const DLayout &dl, void *ws, hipStream_t s) {
+    BArgs ba{};
+    char *w = static_cast<char *>(ws);
+    ba.segs = segs;
+    ba.wl = dl.g;
+    ba.ws = ws;
+    ba.fp = reinterpret_cast<FineParams *>(w + dl.fparams);
+    ba.fcell = reinterpret_cast<int2 *>(w + dl.fcell);
+    ba.tsum = reinterpret_cast<int *>(w + dl.tsum);
+    ba.pool = reinterpret_cast<Cand *>(w + dl.pool);
+    for (int l = 0; l <= segs.L; ++l) {
+        ba.fc_off[l] = dl.fc_off[l];
+        ba.tile_off[l] = dl.tile_off[l];
+        if (l < segs.L) ba.fcmax[l] = dl.fcmax[l];
     }
+    ba.fc_per_b = dl.fc_per_b;
+    ba.pool_per_b = dl.pool_per_b;
+    ba.tt_per_b = dl.tt_per_b;
+    ba.K = a.K;
+    const unsigned nbuild = (unsigned)(a.B * dl.tt_per_b);
+    hipLaunchKernelGGL((cand_count_kernel<KT>), dim3(nbuild), dim3(CB), 0, s, ba);
+    hipLaunchKernelGGL((cand_fill_kernel<KT>), dim3(nbuild), dim3(CB), 0, s, ba);
+
+    CArgs ka{};
+    ka.a = a;
+    ka.segs = segs;
+    ka.wl = dl.g;
+    ka.ws = ws;
+    ka.fp = ba.fp;
+    ka.fcell = ba.fcell;
+    ka.pool = ba.pool;
+    for (int l = 0; l <= segs.L; ++l) ka.fc_off[l] = dl.fc_off[l];
+    ka.fc_per_b = dl.fc_per_b;
+    ka.pool_per_b = dl.pool_per_b;
+    int pl = 0;
+    while ((1 << pl) < a.P) ++pl;
+    ka.pl_log2 = pl;
+    const int RW = 64 >> pl;
+    const size_t per_wave = sizeof(int2) * (size_t)RW * a.L * a.P * a.K;  // <= 32 KB (L * P <= 32, K <= 8)
+    const int nwv = per_wave * 4 <= 65536 ? 4 : 1;
+    const int64_t rows = (int64_t)a.B * a.Nq * a.H;
+    const int64_t blocks = (rows + (int64_t)RW * nwv - 1) / ((int64_t)RW * nwv);
+    hipLaunchKernelGGL((deform_cand_kernel<T, KT>), dim3((unsigned)blocks), dim3(64 * nwv), per_wave * nwv, s, ka);
     return check_launch("aff_deform_fwd");
 }
 
 template <typename T>
-aff_status launch_deform(const KArgs &ka, int spr, hipStream_t s) {
-    const int K = ka.a.K;
-    if (K <= 3) return launch_deform_k<T, 3>(ka, spr, s);
-    if (K <= 4) return launch_deform_k<T, 4>(ka, spr, s);
-    return launch_deform_k<T, KMAX>(ka, spr, s);
+aff_status launch_deform(const aff_deform_args &a, const Segs &segs, const DLayout &dl, void *ws, hipStream_t s) {
+    if (a.K <= 3) return launch_deform_k<T, 3>(a, segs, dl, ws, s);
+    if (a.K <= 4) return launch_deform_k<T, 4>(a, segs, dl, ws, s);
+    return launch_deform_k<T, KMAX>(a, segs, dl, ws, s);
 }
 
 template <typename T>
@@ -725,7 +827,7 @@ extern "C" size_t aff_deform_workspace_bytes(const aff_deform_args *args) {
     if (!args || args->L < 1 || args->L > AFF_DEFORM_MAX_LEVELS || args->B <= 0) return 0;
     grid::Segs segs;
     if (deform::check_common(*args, segs) != AFF_OK) return 0;
-    return grid::ws_layout(args->B, segs).total;
+    return deform::d_layout(args->B, segs, args->K).total;
 }
 
 extern "C" aff_status aff_deform_fwd(const aff_deform_args *args, void *ws, size_t ws_bytes, aff_stream_t stream) {
@@ -747,19 +849,18 @@ extern "C" aff_status aff_deform_fwd(const aff_deform_args *args, void *ws, size
     for (int64_t s : {a.v_sb, a.v_sn, a.v_sh, a.o_sb, a.o_sn, a.o_sh})
         AFF_CHECK_ARG((s * esz) % 16 == 0, "aff_deform_fwd: value/output strides must keep 16-byte rows");
     AFF_CHECK_ARG(deform::a16(a.values) && deform::a16(a.out), "aff_deform_fwd: values/out must be 16-byte aligned");
-    const int spr = deform::pow2_at_least(a.L * a.P);
-    if (spr > 32) return fail(AFF_ERR_UNSUPPORTED, "aff_deform_fwd: L*P=%d exceeds 32 samples per head", a.L * a.P);
-    const grid::WsLayout wl = grid::ws_layout(a.B, segs);
-    if (!ws || ws_bytes < wl.total)
-        return fail(AFF_ERR_WORKSPACE, "aff_deform_fwd: workspace of %zu bytes needed, got %zu", wl.total, ws_bytes);
+    if (a.L * a.P > 32) return fail(AFF_ERR_UNSUPPORTED, "aff_deform_fwd: L*P=%d exceeds 32 samples per head", a.L * a.P);
+    const deform::DLayout dl = deform::d_layout(a.B, segs, a.K);
+    if (!ws || ws_bytes < dl.total)
+        return fail(AFF_ERR_WORKSPACE, "aff_deform_fwd: workspace of %zu bytes needed, got %zu", dl.total, ws_bytes);
     AFF_CHECK_ARG((reinterpret_cast<uintptr_t>(ws) & 255) == 0, "aff_deform_fwd: workspace must be 256-byte aligned");
+    AFF_CHECK_ARG((int64_t)a.B * dl.tt_per_b < ((int64_t)1 << 31), "aff_deform_fwd: too many build tiles");
     hipStream_t s = static_cast<hipStream_t>(stream);
     st = grid::launch_build(a.kv_pos, a.kp_sb, a.kp_sn, a.B, segs, ws, s);
     if (st != AFF_OK) return st;
-    deform::KArgs ka{a, segs, wl, ws};
-    if (a.dtype == AFF_F32) return deform::launch_deform<float>(ka, spr, s);
-    if (a.dtype == AFF_BF16) return deform::launch_deform<bf16_t>(ka, spr, s);
-    return deform::launch_deform<f16_t>(ka, spr, s);
+    if (a.dtype == AFF_F32) return deform::launch_deform<float>(a, segs, dl, ws, s);
+    if (a.dtype == AFF_BF16) return deform::launch_deform<bf16_t>(a, segs, dl, ws, s);
+    return deform::launch_deform<f16_t>(a, segs, dl, ws, s);
 }
 
 extern "C" aff_status aff_deform_sample_fwd(int eps_mode, const float *sampling_locs, int64_t l_sb, int64_t l_sn,

@@ -127,6 +127,51 @@ def test_cfg4_single_level_shepard(oracle_mod, dev):
     _close(out, ro, torch.bfloat16)
 
 
+def _edge_points(name, B, N, g):
+    if name == "lattice_ties":        # exact fp32 lattice with duplicates: many equal distances
+        return torch.randint(0, 16, (B, N, 2), generator=g).float() / 16
+    if name == "clustered":           # most points in a tiny box: very long candidate lists
+        kv = torch.rand((B, N, 2), generator=g)
+        m = N * 9 // 10
+        kv[:, :m] = 0.4 + torch.rand((B, m, 2), generator=g) * 1e-3
+        return kv
+    if name == "identical":           # zero extent
+        return torch.tensor([0.3, 0.7]).expand(B, N, 2).contiguous()
+    if name == "elongated":           # 100:1 aspect ratio
+        kv = torch.rand((B, N, 2), generator=g)
+        kv[..., 1] *= 0.01
+        return kv
+    return torch.rand((B, N, 2), generator=g)
+
+
+@pytest.mark.parametrize("name,K,off_sd", [("uniform", 3, 0.02), ("lattice_ties", 3, 0.0), ("lattice_ties", 8, 0.0),
+                                           ("clustered", 3, 0.05), ("identical", 4, 0.05), ("elongated", 3, 0.03),
+                                           ("uniform", 8, 0.6)])
+def test_neighbour_search_edge_cases(oracle_mod, dev, name, K, off_sd):
+    """Exact neighbour sets on inputs that stress the fine-cell candidate lists:
+    ties and duplicates, dense clusters (lists beyond their cap), zero extent,
+    elongated sets, and samples far outside the points (off_sd = 0.6)."""
+    print(f"[deform edge] {name} K={K} off_sd={off_sd}", flush=True)
+    g = torch.Generator().manual_seed(11)
+    B, Nq, H, L, P, C = 2, 300, 2, 2, 2, 8
+    sizes = (400, 90)
+    kv = torch.cat([_edge_points(name, B, n, g) for n in sizes], dim=1)
+    if name == "lattice_ties":
+        qp = torch.randint(0, 32, (B, Nq, 2), generator=g).float() / 32
+        off = torch.randint(-4, 5, (B, Nq, H, L, P, 2), generator=g).float() / 64
+    else:
+        qp = torch.rand((B, Nq, 2), generator=g)
+        off = torch.randn((B, Nq, H, L, P, 2), generator=g) * off_sd
+    att = torch.softmax(torch.randn((B, Nq, H, L * P), generator=g), -1).reshape(B, Nq, H, L, P)
+    val = torch.randn((B, sum(sizes), H, C), generator=g)
+    ls = [0, sizes[0], sizes[0] + sizes[1]]
+    out, ki, kd = ms_deformable_attention(qp.to(dev), kv.to(dev), ls, off.to(dev), att.to(dev), val.to(dev),
+                                          power=2.0, k=K, weighting="idw", return_knn=True)
+    ro, ri = oracle_mod.deform(qp.numpy(), kv.numpy(), ls, off.numpy(), att.numpy(), val.numpy(), 2.0, K, "idw")
+    np.testing.assert_array_equal(ki.cpu().numpy(), ri)
+    _close(out, ro, torch.float32)
+
+
 def test_given_index_kernels(oracle_mod, dev):
     g = torch.Generator().manual_seed(4)
     B, N, Nkv, K, C = 2, 300, 400, 4, 24
