@@ -34,7 +34,8 @@ using namespace grid;
 
 constexpr int THREADS = 256;
 constexpr int KMAX = 8;    // neighbours per sample
-constexpr int NB = 8;
+constexpr int NB = 8;      // value rows in flight per lane (given-index kernels)
+constexpr int PAIR_GROUP = 16;  // the deformable gather's rows in flight per lane; pair lists pad to a multiple
 
 // Fine-cell candidate lists.  Every (image, level) gets a second, finer grid
 // (cells of FINE x FINE per coarse cell, FPAD coarse cells of margin around
@@ -388,85 +389,142 @@ struct CArgs {
     int fc_off[MAX_SEGS + 1];
     int64_t fc_per_b, pool_per_b;
     int pl_log2;  // lanes per row = 2^pl_log2 >= P
+    int osz, asz;  // bytes per offset / attention element
 };
 
+// Raw bits of a sample's offset pair and attention weight, read with
+// dtype-independent instructions: a 16-bit pair is one dword (read twice), an
+// fp32 pair two; a 16-bit weight one half-word (read twice), an fp32 weight
+// two.  Nothing is read outside the element.
+__device__ __forceinline__ void load_sample_raw(const char *op, const char *ap, int osz, int asz, uint32_t &o0,
+                                                uint32_t &o1, uint32_t &at) {
+    o0 = *reinterpret_cast<const uint32_t *>(op);
+    o1 = *reinterpret_cast<const uint32_t *>(op + (osz == 4 ? 4 : 0));
+    const uint32_t lo = *reinterpret_cast<const uint16_t *>(ap);
+    const uint32_t hi = *reinterpret_cast<const uint16_t *>(ap + (asz == 4 ? 2 : 0));
+    at = lo | (hi << 16);
+}
+
+__device__ __forceinline__ float raw_to_float(uint32_t v, int dtype) {
+    if (dtype == AFF_F32) return __uint_as_float(v);
+    if (dtype == AFF_BF16) return __uint_as_float(v << 16);
+    return float(__builtin_bit_cast(_Float16, uint16_t(v)));
+}
+
 // One wave = RW = 64 / PL consecutive (b, q, h) rows.  Search: lane (r, p)
-// takes sample (l, p) of row r for every level l, scans its fine cell's list
-// (or the coarse grid outside the fine grid) and stages (row, attn * w) of its
-// K neighbours in the wave's LDS slice.  Gather: lane (r, chunk) sums the
-// row's L * P * K value rows over 8 channels (16-byte loads) in fp32.  Waves
-// share nothing; the workgroup only batches them.
-template <typename T, int KT>
+// takes sample (l, p) of row r for every level l.  Every level's sample
+// (offset, weight, fine-cell parameters) is read first, then every level's
+// cell entry, so those reads overlap; then each level's list is scanned
+// (four entries per step, the next four in flight) or, outside the fine grid,
+// the coarse grid searched, and (value offset, attn * w) of the K neighbours
+// staged in the wave's LDS slice.  Gather: lane (r, chunk) sums the row's
+// L * P * K value rows over 8 channels (16-byte loads) in fp32.  Waves share
+// nothing; the workgroup only batches them.
+template <typename T, int KT, int LMAX>
 __global__ __launch_bounds__(THREADS) void deform_cand_kernel(const CArgs ka) {
     using IO = ElemIO<T>;
     extern __shared__ int2 s_pair[];
     const aff_deform_args &a = ka.a;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nwv = blockDim.x >> 6;
     const int PL = 1 << ka.pl_log2, RW = 64 >> ka.pl_log2;
-    const int S = a.L * a.P, K = a.K, SK = S * K;
-    int2 *pr = s_pair + wv * RW * SK;
+    const int L = a.L, S = L * a.P, K = a.K, SK = S * K;
+    const int SKP = (SK + PAIR_GROUP - 1) / PAIR_GROUP * PAIR_GROUP;  // pairs per row, padded
+    int2 *pr = s_pair + wv * RW * SKP;
     const int64_t total = (int64_t)a.B * a.Nq * a.H;
     const int64_t row0 = ((int64_t)xcd_swizzle(blockIdx.x, gridDim.x) * nwv + wv) * RW;
     const float pw = *a.power;
+    const int ipow = (pw == 0.f || pw == 1.f || pw == 2.f || pw == 3.f || pw == 4.f) ? int(pw) : -1;
 
     {
         const int r = lane >> ka.pl_log2, p = lane & (PL - 1);
         const int64_t row = row0 + r;
         const bool act = row < total && p < a.P;
         const uint32_t rw = act ? uint32_t(row) : 0u;  // the host keeps B * Nq * H below 2^31
+        const int pc = act ? p : 0;
         const int h = int(rw % uint32_t(a.H));
         const uint32_t bq = rw / uint32_t(a.H);
         const int q = int(bq % uint32_t(a.Nq)), b = int(bq / uint32_t(a.Nq));
-        float qx = 0.f, qy = 0.f;
-        if (act) {
-            qx = a.query_pos[(int64_t)b * a.qp_sb + (int64_t)q * a.qp_sn];
-            qy = a.query_pos[(int64_t)b * a.qp_sb + (int64_t)q * a.qp_sn + 1];
+        const float qx = a.query_pos[(int64_t)b * a.qp_sb + (int64_t)q * a.qp_sn];
+        const float qy = a.query_pos[(int64_t)b * a.qp_sb + (int64_t)q * a.qp_sn + 1];
+        const char *ob = static_cast<const char *>(a.offsets) +
+                         ((int64_t)b * a.off_sb + (int64_t)q * a.off_sn + (int64_t)h * a.off_sh) * ka.osz;
+        const char *abase = static_cast<const char *>(a.attn) +
+                            ((int64_t)b * a.at_sb + (int64_t)q * a.at_sn + (int64_t)h * a.at_sh) * ka.asz;
+        const int2 *fc_b = ka.fcell + b * ka.fc_per_b;
+        const FineParams *fp_b = ka.fp + b * L;
+        const int vrow = h * int(a.v_sh);  // value offset of head h (elements; the host keeps it below 2^31)
+        if (act && p == 0)  // the row's padding pairs: a valid row with weight 0
+            for (int j = SK; j < SKP; ++j) pr[r * SKP + j] = make_int2(vrow, 0);
+
+        // ---- every level's sample and fine-grid parameters (levels >= L repeat level L - 1)
+        uint32_t o0[LMAX], o1[LMAX], at[LMAX];
+        float4 fpa[LMAX];
+        int2 fpg[LMAX];
+#pragma unroll
+        for (int l = 0; l < LMAX; ++l) {
+            const int lc = min(l, L - 1);
+            const int s = lc * a.P + pc;
+            load_sample_raw(ob + s * 2 * ka.osz, abase + s * ka.asz, ka.osz, ka.asz, o0[l], o1[l], at[l]);
+            const FineParams *f = fp_b + lc;
+            fpa[l] = *reinterpret_cast<const float4 *>(f);
+            fpg[l] = *reinterpret_cast<const int2 *>(&f->gx);
         }
-        const int64_t ob = (int64_t)b * a.off_sb + (int64_t)q * a.off_sn + (int64_t)h * a.off_sh;
-        const int64_t ab = (int64_t)b * a.at_sb + (int64_t)q * a.at_sn + (int64_t)h * a.at_sh;
-        for (int l = 0; l < a.L; ++l) {
+        // ---- sample locations and every level's cell entry
+        float sxl[LMAX], syl[LMAX];
+        int2 ce[LMAX];
+        bool inside[LMAX];
+#pragma unroll
+        for (int l = 0; l < LMAX; ++l) {
+#pragma clang fp contract(off)
+            const int lc = min(l, L - 1);
+            sxl[l] = qx + raw_to_float(o0[l], a.off_dtype);
+            syl[l] = qy + raw_to_float(a.off_dtype == AFF_F32 ? o1[l] : o0[l] >> 16, a.off_dtype);
+            const float fx = floorf(__fmul_rn(__fsub_rn(sxl[l], fpa[l].x), fpa[l].w));
+            const float fy = floorf(__fmul_rn(__fsub_rn(syl[l], fpa[l].y), fpa[l].w));
+            inside[l] = fx >= 0.f && fx < float(fpg[l].x) && fy >= 0.f && fy < float(fpg[l].y);
+            const int cell = inside[l] ? int(fy) * fpg[l].x + int(fx) : 0;
+            ce[l] = fc_b[ka.fc_off[lc] + cell];
+        }
+
+        // Levels in turn: level l's values sit at index 0 of the staged arrays,
+        // which shift down by one after each level (constant indices keep
+        // them in registers with a runtime level loop).
+        for (int l = 0; l < L; ++l) {
             const int s = l * a.P + p;
             const int lstart = ka.segs.start[l];
             const int keff = min(K, ka.segs.start[l + 1] - lstart);
+            const float sx = sxl[0], sy = syl[0];
             uint64_t keys[KT];
 #pragma unroll
             for (int j = 0; j < KT; ++j) keys[j] = ~0ull;
-            float aw = 0.f;
-            if (act && keff > 0) {
-                const float sx = qx + load_any(a.offsets, a.off_dtype, ob + s * 2);
-                const float sy = qy + load_any(a.offsets, a.off_dtype, ob + s * 2 + 1);
-                aw = load_any(a.attn, a.attn_dtype, ab + s);
-                const FineParams f = ka.fp[b * a.L + l];
-                int beg = 0, cnt = -1;
-                {
-#pragma clang fp contract(off)
-                    const float fx = floorf(__fmul_rn(__fsub_rn(sx, f.x0), f.inv_s));
-                    const float fy = floorf(__fmul_rn(__fsub_rn(sy, f.y0), f.inv_s));
-                    if (fx >= 0.f && fx < float(f.gx) && fy >= 0.f && fy < float(f.gy)) {
-                        const int2 e = ka.fcell[b * ka.fc_per_b + ka.fc_off[l] + int(fy) * f.gx + int(fx)];
-                        beg = e.x;
-                        cnt = e.y;
-                    }
-                }
-                if (cnt > 0) {
-                    const Cand *cp = ka.pool + b * ka.pool_per_b + beg;
-                    for (int i = 0; i < cnt; i += 4) {
-                        Cand c4[4];
+            const int cnt = act && keff > 0 ? (inside[0] ? ce[0].y : -1) : 0;
+            if (cnt > 0) {
+                // Four entries per step, the next four loaded during this step.
+                // Lanes past their list's end all read the pool's first entry:
+                // one L1 access between them instead of one each.
+                const Cand *cp = ka.pool + b * ka.pool_per_b + ce[0].x;
+                Cand c4[4];
 #pragma unroll
-                        for (int u = 0; u < 4; ++u) c4[u] = cp[min(i + u, cnt - 1)];
+                for (int u = 0; u < 4; ++u) c4[u] = u < cnt ? cp[u] : ka.pool[0];
+                for (int i = 0; i < cnt; i += 4) {
+                    Cand n4[4];
 #pragma unroll
-                        for (int u = 0; u < 4; ++u)
-                            if (i + u < cnt) topk_insert<KT>(keys, make_key(dist2(c4[u].x, c4[u].y, sx, sy), c4[u].row));
-                    }
-                } else {
-                    const SegView g = seg_view(ka.ws, ka.wl, ka.segs, b, l);
-                    const float area = float(g.p.gx) * float(g.p.gy) * g.p.h * g.p.h;
-                    const float rho = float(g.n) / fmaxf(area, 1e-30f);
-                    const float U0 = keff >= g.n ? INFINITY : fmaxf(float(keff + 4) / (3.14159265f * rho), 1e-30f);
-                    topk_global<KT>(g, sx, sy, U0, keff, keys);
+                    for (int u = 0; u < 4; ++u) n4[u] = i + 4 + u < cnt ? cp[i + 4 + u] : ka.pool[0];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        if (i + u < cnt) topk_insert<KT>(keys, make_key(dist2(c4[u].x, c4[u].y, sx, sy), c4[u].row));
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) c4[u] = n4[u];
                 }
+            } else if (cnt < 0) {
+                const SegView g = seg_view(ka.ws, ka.wl, ka.segs, b, l);
+                const float area = float(g.p.gx) * float(g.p.gy) * g.p.h * g.p.h;
+                const float rho = float(g.n) / fmaxf(area, 1e-30f);
+                const float U0 = keff >= g.n ? INFINITY : fmaxf(float(keff + 4) / (3.14159265f * rho), 1e-30f);
+                topk_global<KT>(g, sx, sy, U0, keff, keys);
             }
             if (act) {
+                const float aw = raw_to_float(at[0], a.attn_dtype);
                 float wj[KT];
                 float wsum = 0.f;
                 if (a.mode == AFF_DEFORM_SHEPARD) {
@@ -474,7 +532,7 @@ __global__ __launch_bounds__(THREADS) void deform_cand_kernel(const CArgs ka) {
                     float lg[KT], mx = -INFINITY;
 #pragma unroll
                     for (int j = 0; j < KT; ++j) {
-                        lg[j] = j < keff ? -pp * (sqrtf(key_d2(keys[j])) + 1e-6f) : -INFINITY;
+                        lg[j] = j < keff ? -pp * (__builtin_amdgcn_sqrtf(key_d2(keys[j])) + 1e-6f) : -INFINITY;
                         mx = fmaxf(mx, lg[j]);
                     }
 #pragma unroll
@@ -484,25 +542,52 @@ __global__ __launch_bounds__(THREADS) void deform_cand_kernel(const CArgs ka) {
                     }
                     wsum += 1e-8f;
                 } else {
+                    // d2^power: a product chain for the integer powers 0..4 (exact to a few
+                    // ulp), exp2(power * log2(d2)) otherwise
 #pragma unroll
                     for (int j = 0; j < KT; ++j) {
-                        wj[j] = j < keff ? 1.f / (__powf(key_d2(keys[j]), pw) + 1e-10f) : 0.f;
+                        const float d2 = key_d2(keys[j]);
+                        float pv;
+                        if (ipow == 0) pv = 1.f;
+                        else if (ipow == 1) pv = d2;
+                        else if (ipow == 2) pv = d2 * d2;
+                        else if (ipow == 3) pv = d2 * d2 * d2;
+                        else if (ipow == 4) pv = (d2 * d2) * (d2 * d2);
+                        else pv = __builtin_amdgcn_exp2f(pw * __builtin_amdgcn_logf(d2));
+                        wj[j] = j < keff ? __builtin_amdgcn_rcpf(pv + 1e-10f) : 0.f;
                         wsum += wj[j];
                     }
                     wsum += 1e-12f;
                 }
-                const float inv = 1.f / wsum;
-                int2 *dst = pr + r * SK + s * K;
-                const int64_t kb = (row * S + s) * K;  // [B, Nq, H, L, P, K]
+                const float inv = __builtin_amdgcn_rcpf(wsum);
+                int2 *dst = pr + r * SKP + s * K;
 #pragma unroll
                 for (int j = 0; j < KT; ++j) {
                     if (j < K) {
                         const bool ok = j < keff;
-                        dst[j] = make_int2(ok ? key_index(keys[j]) : -1, __float_as_int(ok ? aw * wj[j] * inv : 0.f));
-                        if (a.knn_idx) a.knn_idx[kb + j] = ok ? key_index(keys[j]) - lstart : -1;
-                        if (a.knn_d2) a.knn_d2[kb + j] = ok ? key_d2(keys[j]) : INFINITY;
+                        dst[j] = make_int2(ok ? key_index(keys[j]) * int(a.v_sn) + vrow : vrow,
+                                           __float_as_int(ok ? aw * wj[j] * inv : 0.f));
                     }
                 }
+                if (a.knn_idx || a.knn_d2) {
+                    const int64_t kb = (row * S + s) * K;  // [B, Nq, H, L, P, K]
+#pragma unroll
+                    for (int j = 0; j < KT; ++j) {
+                        if (j < K) {
+                            const bool ok = j < keff;
+                            if (a.knn_idx) a.knn_idx[kb + j] = ok ? key_index(keys[j]) - lstart : -1;
+                            if (a.knn_d2) a.knn_d2[kb + j] = ok ? key_d2(keys[j]) : INFINITY;
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i + 1 < LMAX; ++i) {
+                sxl[i] = sxl[i + 1];
+                syl[i] = syl[i + 1];
+                ce[i] = ce[i + 1];
+                inside[i] = inside[i + 1];
+                at[i] = at[i + 1];
             }
         }
     }
@@ -510,6 +595,10 @@ __global__ __launch_bounds__(THREADS) void deform_cand_kernel(const CArgs ka) {
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
+    // ---- gather: pairs (value offset of (row, head) in elements, weight), padded
+    // to SKP with weight-0 pairs; GB rows in flight per lane, pairs read two per
+    // LDS access
+    constexpr int GB = sizeof(T) == 2 ? PAIR_GROUP : PAIR_GROUP / 2;
     const int CG = a.C / 8;
     for (int it = lane; it < RW * CG; it += 64) {
         const int rr = it / CG, cc = it - rr * CG;
@@ -519,28 +608,29 @@ __global__ __launch_bounds__(THREADS) void deform_cand_kernel(const CArgs ka) {
         const int h = int(rw % uint32_t(a.H));
         const uint32_t bq = rw / uint32_t(a.H);
         const int q = int(bq % uint32_t(a.Nq)), b = int(bq / uint32_t(a.Nq));
-        const T *V = static_cast<const T *>(a.values) + (int64_t)b * a.v_sb + (int64_t)h * a.v_sh + cc * 8;
+        const T *V = static_cast<const T *>(a.values) + (int64_t)b * a.v_sb + cc * 8;
         T *O = static_cast<T *>(a.out) + (int64_t)b * a.o_sb + (int64_t)q * a.o_sn + (int64_t)h * a.o_sh + cc * 8;
-        const int2 *pp = pr + rr * SK;
+        const int4 *pp = reinterpret_cast<const int4 *>(pr + rr * SKP);
         float acc[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-        for (int j0 = 0; j0 < SK; j0 += NB) {
-            typename IO::raw8 fr[NB];
-            float wv[NB];
+        for (int j0 = 0; j0 < SKP; j0 += GB) {
+            int4 e2[GB / 2];
 #pragma unroll
-            for (int u = 0; u < NB; ++u) {
-                const int j = j0 + u;
-                const int2 e = j < SK ? pp[j] : make_int2(-1, 0);
-                wv[u] = e.x >= 0 ? __int_as_float(e.y) : 0.f;
-                fr[u] = IO::load_raw(V + (int64_t)(e.x >= 0 ? e.x : 0) * a.v_sn);
+            for (int u = 0; u < GB / 2; ++u) e2[u] = pp[j0 / 2 + u];
+            typename IO::raw8 fr[GB];
+#pragma unroll
+            for (int u = 0; u < GB / 2; ++u) {
+                fr[2 * u] = IO::load_raw(V + (uint32_t)e2[u].x);
+                fr[2 * u + 1] = IO::load_raw(V + (uint32_t)e2[u].z);
             }
 #pragma unroll
-            for (int u = 0; u < NB; ++u) {
+            for (int u = 0; u < GB; ++u) {
                 float fv[8];
                 IO::cvt(fr[u], fv);
+                const float wv = __int_as_float(u & 1 ? e2[u / 2].w : e2[u / 2].y);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) acc[e] += wv[u] * fv[e];
+                for (int e = 0; e < 8; ++e) acc[e] += wv * fv[e];
             }
         }
         IO::store8(O, acc);
@@ -756,15 +846,24 @@ aff_status launch_deform_k(const aff_deform_args &a, const Segs &segs, const DLa
     for (int l = 0; l <= segs.L; ++l) ka.fc_off[l] = dl.fc_off[l];
     ka.fc_per_b = dl.fc_per_b;
     ka.pool_per_b = dl.pool_per_b;
+    ka.osz = a.off_dtype == AFF_F32 ? 4 : 2;
+    ka.asz = a.attn_dtype == AFF_F32 ? 4 : 2;
     int pl = 0;
     while ((1 << pl) < a.P) ++pl;
     ka.pl_log2 = pl;
     const int RW = 64 >> pl;
-    const size_t per_wave = sizeof(int2) * (size_t)RW * a.L * a.P * a.K;  // <= 32 KB (L * P <= 32, K <= 8)
+    const int SKP = (a.L * a.P * a.K + PAIR_GROUP - 1) / PAIR_GROUP * PAIR_GROUP;
+    const size_t per_wave = sizeof(int2) * (size_t)RW * SKP;  // <= 32 KB (L * P <= 32, K <= 8)
     const int nwv = per_wave * 4 <= 65536 ? 4 : 1;
     const int64_t rows = (int64_t)a.B * a.Nq * a.H;
     const int64_t blocks = (rows + (int64_t)RW * nwv - 1) / ((int64_t)RW * nwv);
-    hipLaunchKernelGGL((deform_cand_kernel<T, KT>), dim3((unsigned)blocks), dim3(64 * nwv), per_wave * nwv, s, ka);
+    const dim3 grid((unsigned)blocks), block(64 * nwv);
+    if (a.L == 1)
+        hipLaunchKernelGGL((deform_cand_kernel<T, KT, 1>), grid, block, per_wave * nwv, s, ka);
+    else if (a.L <= 4)
+        hipLaunchKernelGGL((deform_cand_kernel<T, KT, 4>), grid, block, per_wave * nwv, s, ka);
+    else
+        hipLaunchKernelGGL((deform_cand_kernel<T, KT, 8>), grid, block, per_wave * nwv, s, ka);
     return check_launch("aff_deform_fwd");
 }
 
@@ -849,6 +948,14 @@ extern "C" aff_status aff_deform_fwd(const aff_deform_args *args, void *ws, size
     for (int64_t s : {a.v_sb, a.v_sn, a.v_sh, a.o_sb, a.o_sn, a.o_sh})
         AFF_CHECK_ARG((s * esz) % 16 == 0, "aff_deform_fwd: value/output strides must keep 16-byte rows");
     AFF_CHECK_ARG(deform::a16(a.values) && deform::a16(a.out), "aff_deform_fwd: values/out must be 16-byte aligned");
+    // offset pairs are read as dwords: 4-byte aligned pairs
+    const int osz = a.off_dtype == AFF_F32 ? 4 : 2;
+    AFF_CHECK_ARG((reinterpret_cast<uintptr_t>(a.offsets) & 3) == 0 &&
+                      ((a.off_sb | a.off_sn | a.off_sh) * osz) % 4 == 0,
+                  "aff_deform_fwd: offsets must be 4-byte aligned with even strides");
+    AFF_CHECK_ARG((int64_t)(a.level_start[a.L] > 0 ? a.level_start[a.L] - 1 : 0) * a.v_sn + (int64_t)(a.H - 1) * a.v_sh +
+                      a.C < ((int64_t)1 << 31),
+                  "aff_deform_fwd: one image's values must span fewer than 2^31 elements");
     if (a.L * a.P > 32) return fail(AFF_ERR_UNSUPPORTED, "aff_deform_fwd: L*P=%d exceeds 32 samples per head", a.L * a.P);
     const deform::DLayout dl = deform::d_layout(a.B, segs, a.K);
     if (!ws || ws_bytes < dl.total)
