@@ -8,14 +8,15 @@
 //   mode IDW:     w_j = (1 / (d2_j^power + 1e-10)) / (sum + 1e-12)
 //                 (inverse_distance_weighting, src/utils/geometry.py:40-53, on squared distances)
 //   out[b, q, h, :] = sum_s attn[b, q, h, s] * sum_j w_j * values[b, level_row(l, j), h, :]
-// Three launches after the coarse grid build (grid2d.hpp): cand_count_kernel
-// and cand_fill_kernel write, for every cell of a finer grid over each level,
-// the list of points that can be among the K nearest of any location in the
-// cell; deform_cand_kernel then gives each sample one lane that scans its
-// cell's list (exact (d2, row) keys), stages (row, attn * w) pairs in the
-// wave's LDS slice, and gathers the value rows (8 channels per lane, 16-byte
-// loads) in fp32.  The neighbour indices never go to HBM unless the caller
-// asks for them.
+// Two launches after the coarse grid build (grid2d.hpp): cand_build_kernel
+// writes, for every cell of a finer grid over each level, the list of points
+// that can be among the K nearest of any location in the cell (nearest first,
+// with lower bounds on the distances); deform_cand_kernel then gives each
+// sample one lane that scans its cell's list (exact (d2, row) keys) until the
+// bounds pass its K-th distance, stages (row, attn * w) pairs in the wave's
+// LDS slice, and gathers the value rows (8 channels per lane, 16-byte loads)
+// in fp32.  The neighbour indices never go to HBM unless the caller asks for
+// them.
 //
 // aff_deform_sample_fwd: the same weights from given neighbour indices
 //   (fused_deformable_attention, fused_deform_attn.py:79-231, 503-571: sqrt(d2) + 1e-6;
@@ -57,17 +58,21 @@ struct FineParams {
     int pad;
 };
 
+// A list entry: the point and its row in the image's level concatenation.  A
+// list starts with its HEAD points nearest to the cell sorted by that distance
+// (the head), so within the head the distance of an entry to the cell bounds
+// the distances of every later entry from below.
 struct Cand {
     float x, y;
-    int row;  // row of the point in the image's level concatenation
+    int row;
 };
 
 // Workspace of aff_deform_fwd: the coarse grids (grid2d.hpp), then the fine
-// grids' parameters, their (begin, count) cell tables, the per-tile candidate
-// counts and the candidate pool of each batch item.
+// grids' parameters, their (begin, count) cell tables, one pool allocation
+// counter per batch item (zeroed by the grid build) and the candidate pools.
 struct DLayout {
     WsLayout g;
-    size_t fparams, fcell, tsum, pool, total;
+    size_t fparams, fcell, counter, pool, total;
     int fc_off[MAX_SEGS + 1];    // fine-cell table offset of each level (int2 entries)
     int fcmax[MAX_SEGS];         // fine cells reserved per level
     int tile_off[MAX_SEGS + 1];  // first build tile of each level
@@ -100,11 +105,11 @@ inline DLayout d_layout(int B, const Segs &s, int K) {
     d.tt_per_b = tt;
     d.fcell = off;
     off = align256(off + sizeof(int2) * (size_t)B * fc);
-    d.tsum = off;
-    off = align256(off + sizeof(int) * (size_t)B * tt);
+    d.counter = off;
+    off = align256(off + sizeof(int) * (size_t)B);
     d.pool_per_b = (int64_t)pool_per_point(K) * s.npts_b + 1024;
-    d.pool = off;
-    off = align256(off + sizeof(Cand) * (size_t)B * (size_t)d.pool_per_b);
+    d.pool = off;  // + 4 entries: a scan's read-ahead past the last list stays inside
+    off = align256(off + sizeof(Cand) * ((size_t)B * (size_t)d.pool_per_b + 4));
     d.total = off;
     return d;
 }
@@ -222,16 +227,21 @@ __device__ __forceinline__ float cell_bound(const SegView &g, const Rect &rc, in
     const int ccy = cell_coord(0.5f * (rc.y0 + rc.y1), p.y0, p.inv_h, p.gy);
     auto visit = [&](int cy, int cx0, int cx1) {
         const int beg = g.cs[cy * p.gx + cx0], end = g.cs[cy * p.gx + cx1 + 1];
-        for (int t = beg; t < end; ++t) {
-            const float4 pt = g.P[t];
-            const float mx = fmaxf(fabsf(pt.x - rc.x0), fabsf(pt.x - rc.x1));
-            const float my = fmaxf(fabsf(pt.y - rc.y0), fabsf(pt.y - rc.y1));
-            float v = mx * mx + my * my;
+        for (int t = beg; t < end; t += 4) {  // four loads in flight per step
+            float4 pt[4];
 #pragma unroll
-            for (int i = 0; i < KT; ++i) {
-                const float lo = fminf(top[i], v);
-                v = fmaxf(top[i], v);
-                top[i] = lo;
+            for (int u = 0; u < 4; ++u) pt[u] = g.P[min(t + u, end - 1)];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float mx = fmaxf(fabsf(pt[u].x - rc.x0), fabsf(pt[u].x - rc.x1));
+                const float my = fmaxf(fabsf(pt[u].y - rc.y0), fabsf(pt[u].y - rc.y1));
+                float v = t + u < end ? mx * mx + my * my : INFINITY;
+#pragma unroll
+                for (int i = 0; i < KT; ++i) {
+                    const float lo = fminf(top[i], v);
+                    v = fmaxf(top[i], v);
+                    top[i] = lo;
+                }
             }
         }
         found += end - beg;
@@ -257,8 +267,9 @@ __device__ __forceinline__ float cell_bound(const SegView &g, const Rect &rc, in
     return R * 1.0001f + 1e-30f;
 }
 
-// Calls f(point) for every point of the level whose distance^2 to the
-// rectangle is at most R, in the coarse grid's cell order.
+// Calls f(point, distance^2 to the rectangle) for every point of the level
+// whose distance^2 to the rectangle is at most R, in the coarse grid's cell
+// order.
 template <typename F>
 __device__ __forceinline__ void visit_cands(const SegView &g, const Rect &rc, float R, F &&f) {
 #pragma clang fp contract(off)
@@ -268,11 +279,17 @@ __device__ __forceinline__ void visit_cands(const SegView &g, const Rect &rc, fl
     const int cx0 = cell_coord(rc.x0 - rr, p.x0, p.inv_h, p.gx), cx1 = cell_coord(rc.x1 + rr, p.x0, p.inv_h, p.gx);
     for (int cy = cy0; cy <= cy1; ++cy) {
         const int beg = g.cs[cy * p.gx + cx0], end = g.cs[cy * p.gx + cx1 + 1];
-        for (int t = beg; t < end; ++t) {
-            const float4 pt = g.P[t];
-            const float dx = fmaxf(0.f, fmaxf(rc.x0 - pt.x, pt.x - rc.x1));
-            const float dy = fmaxf(0.f, fmaxf(rc.y0 - pt.y, pt.y - rc.y1));
-            if (dx * dx + dy * dy <= R) f(pt);
+        for (int t = beg; t < end; t += 4) {  // four loads in flight per step
+            float4 pt[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) pt[u] = g.P[min(t + u, end - 1)];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float dx = fmaxf(0.f, fmaxf(rc.x0 - pt[u].x, pt[u].x - rc.x1));
+                const float dy = fmaxf(0.f, fmaxf(rc.y0 - pt[u].y, pt[u].y - rc.y1));
+                const float md = dx * dx + dy * dy;
+                if (t + u < end && md <= R) f(pt[u], md);
+            }
         }
     }
 }
@@ -282,8 +299,8 @@ struct BArgs {
     WsLayout wl;
     const void *ws;
     FineParams *fp;  // [B * L]
-    int2 *fcell;     // [B][fc_per_b]: (R bits, count) after the count pass, (begin, count) after the fill
-    int *tsum;       // [B][tt_per_b]
+    int2 *fcell;     // [B][fc_per_b]: (begin, count) of each fine cell's list
+    int *counter;    // [B]: pool entries handed out per batch item
     Cand *pool;      // [B][pool_per_b]
     int fc_off[MAX_SEGS + 1], fcmax[MAX_SEGS], tile_off[MAX_SEGS + 1];
     int64_t fc_per_b, pool_per_b;
@@ -316,65 +333,84 @@ __device__ __forceinline__ void tile_of(const BArgs &ba, int &b, int &l, int &t,
     t = gt - ba.tile_off[l];
 }
 
-// Pass 1: one lane per fine cell: R and the list length.
+// One lane per fine cell.  Pass 1 over the candidates counts them and keeps
+// their HEAD smallest distances to the cell; the tile's lists then get pool
+// space from the image's counter (one atomic per tile: the layout depends on
+// the order tiles arrive in, the lists do not).  Pass 2 writes each of those
+// HEAD nearest points at its rank among them (the sorted head) and the rest
+// after them in visit order.  Each list is padded to a multiple of 4 entries
+// with points at infinity; its cell entry holds (begin, padded length | head
+// length << 16).  Lists longer than MAX_CAND, or beyond the pool, get count
+// -1: their samples search the coarse grid.
+constexpr int HEAD = 16;
+
 template <int KT>
-__global__ __launch_bounds__(CB) void cand_count_kernel(const BArgs ba) {
+__global__ __launch_bounds__(CB) void cand_build_kernel(const BArgs ba) {
     __shared__ int s_w[4];
+    __shared__ int s_base;
     int b, l, t, gt;
     tile_of(ba, b, l, t, gt);
     const SegView g = seg_view(ba.ws, ba.wl, ba.segs, b, l);
     const FineParams f = fine_params(g.p, g.n, ba.fcmax[l]);
     if (t == 0 && threadIdx.x == 0) ba.fp[b * ba.segs.L + l] = f;
+    const int ncf = f.gx * f.gy;
+    if (t * CB >= ncf) return;  // the whole tile lies beyond the grid
     const int c = t * CB + threadIdx.x;
-    const bool valid = c < f.gx * f.gy;
-    int cnt = 0;
+    const bool valid = c < ncf && g.n > 0;
+    Rect rc{};
     float R = 0.f;
-    if (valid && g.n > 0) {
-        const Rect rc = fine_rect(f, c);
+    int cnt = 0;
+    float top[HEAD];
+#pragma unroll
+    for (int i = 0; i < HEAD; ++i) top[i] = INFINITY;
+    if (valid) {
+        rc = fine_rect(f, c);
         R = cell_bound<KT>(g, rc, min(ba.K, g.n));
-        visit_cands(g, rc, R, [&](const float4 &) { ++cnt; });
-    }
-    if (cnt > MAX_CAND) cnt = -1;
-    if (valid) ba.fcell[b * ba.fc_per_b + ba.fc_off[l] + c] = make_int2(__float_as_int(R), cnt);
-    int tot;
-    block_scan(max(cnt, 0), s_w, &tot);
-    if (threadIdx.x == 0) ba.tsum[b * ba.tt_per_b + gt] = tot;
-}
-
-// Pass 2: list offsets (the counts of all earlier tiles of the image, then
-// this tile's prefix) and the entries.  Lists that do not fit the pool get
-// count -1: their samples search the coarse grid.
-template <int KT>
-__global__ __launch_bounds__(CB) void cand_fill_kernel(const BArgs ba) {
-    __shared__ int s_w[4];
-    int b, l, t, gt;
-    tile_of(ba, b, l, t, gt);
-    const FineParams f = ba.fp[b * ba.segs.L + l];
-    const int c = t * CB + threadIdx.x;
-    if (t * CB >= f.gx * f.gy) return;  // whole tile outside the grid
-    const bool valid = c < f.gx * f.gy;
-    int2 e = valid ? ba.fcell[b * ba.fc_per_b + ba.fc_off[l] + c] : make_int2(0, 0);
-    int before = 0;
-    for (int i = threadIdx.x; i < gt; i += CB) before += ba.tsum[b * ba.tt_per_b + i];
-    int base;
-    block_scan(before, s_w, &base);
-    int tot;
-    const int pre = block_scan(max(e.y, 0), s_w, &tot);
-    const int64_t begin = (int64_t)base + pre;
-    if (!valid) return;
-    int cnt = e.y;
-    if (cnt > 0 && begin + cnt > ba.pool_per_b) cnt = -1;
-    ba.fcell[b * ba.fc_per_b + ba.fc_off[l] + c] = make_int2(int(begin), cnt);
-    if (cnt > 0) {
-        const SegView g = seg_view(ba.ws, ba.wl, ba.segs, b, l);
-        const Rect rc = fine_rect(f, c);
-        Cand *out = ba.pool + b * ba.pool_per_b + begin;
-        int k = 0;
-        visit_cands(g, rc, __int_as_float(e.x), [&](const float4 &pt) {
-            if (k < cnt) out[k] = Cand{pt.x, pt.y, __float_as_int(pt.z)};
-            ++k;
+        visit_cands(g, rc, R, [&](const float4 &, float md) {
+            ++cnt;
+            float v = md;
+#pragma unroll
+            for (int i = 0; i < HEAD; ++i) {
+                const float lo = fminf(top[i], v);
+                v = fmaxf(top[i], v);
+                top[i] = lo;
+            }
         });
     }
+    if (cnt > MAX_CAND) cnt = -1;
+    const int cnt4 = (max(cnt, 0) + 3) & ~3;  // lists padded to whole 4-entry steps
+    int tot;
+    const int pre = block_scan(cnt4, s_w, &tot);
+    if (threadIdx.x == 0) s_base = tot > 0 ? atomicAdd(ba.counter + b, tot) : 0;
+    __syncthreads();
+    if (c >= ncf) return;
+    const int64_t begin = (int64_t)s_base + pre;
+    if (cnt > 0 && begin + cnt4 > ba.pool_per_b) cnt = -1;
+    const int m = min(max(cnt, 0), HEAD);
+    ba.fcell[b * ba.fc_per_b + ba.fc_off[l] + c] = make_int2(cnt > 0 ? int(begin) : 0, cnt > 0 ? cnt4 | (m << 16) : cnt);
+    if (cnt <= 0) return;
+    Cand *out = ba.pool + b * ba.pool_per_b + begin;
+    // padding: points at infinity (their keys lose to every real point)
+    for (int i = cnt; i < cnt4; ++i) out[i] = Cand{INFINITY, INFINITY, -1};
+    float tb = top[0];
+#pragma unroll
+    for (int i = 1; i < HEAD; ++i)
+        if (i < m) tb = top[i];
+    uint32_t used = 0;
+    int tail = m;
+    visit_cands(g, rc, R, [&](const float4 &pt, float md) {
+        int slot = HEAD;
+        if (md <= tb) {
+            int rank = 0;
+#pragma unroll
+            for (int i = 0; i < HEAD; ++i) rank += top[i] < md ? 1 : 0;
+            while (rank < m && ((used >> rank) & 1u)) ++rank;  // equal distances take the next free slot
+            slot = rank;
+        }
+        if (slot < m) used |= 1u << slot;
+        else slot = tail++;
+        if (slot < cnt) out[slot] = Cand{pt.x, pt.y, __float_as_int(pt.z)};
+    });
 }
 
 // --------------------------------------------------------- main kernel --
@@ -415,7 +451,8 @@ __device__ __forceinline__ float raw_to_float(uint32_t v, int dtype) {
 // takes sample (l, p) of row r for every level l.  Every level's sample
 // (offset, weight, fine-cell parameters) is read first, then every level's
 // cell entry, so those reads overlap; then each level's list is scanned
-// (four entries per step, the next four in flight) or, outside the fine grid,
+// (four entries per step, the next four in flight, until the entries' bound
+// passes the K-th distance) or, outside the fine grid,
 // the coarse grid searched, and (value offset, attn * w) of the K neighbours
 // staged in the wave's LDS slice.  Gather: lane (r, chunk) sums the row's
 // L * P * K value rows over 8 channels (16-byte loads) in fp32.  Waves share
@@ -451,40 +488,44 @@ __global__ __launch_bounds__(THREADS) void deform_cand_kernel(const CArgs ka) {
         const char *abase = static_cast<const char *>(a.attn) +
                             ((int64_t)b * a.at_sb + (int64_t)q * a.at_sn + (int64_t)h * a.at_sh) * ka.asz;
         const int2 *fc_b = ka.fcell + b * ka.fc_per_b;
-        const FineParams *fp_b = ka.fp + b * L;
         const int vrow = h * int(a.v_sh);  // value offset of head h (elements; the host keeps it below 2^31)
         if (act && p == 0)  // the row's padding pairs: a valid row with weight 0
             for (int j = SK; j < SKP; ++j) pr[r * SKP + j] = make_int2(vrow, 0);
+        // The fine-grid parameters come through the scalar cache when the wave's
+        // rows all lie in one image (always, unless an image has fewer rows than
+        // a wave), through vector loads otherwise.
+        const int b0 = __builtin_amdgcn_readfirstlane(b);
+        const bool uni = __all(b == b0);
 
-        // ---- every level's sample and fine-grid parameters (levels >= L repeat level L - 1)
+        // ---- every level's sample (levels >= L repeat level L - 1)
         uint32_t o0[LMAX], o1[LMAX], at[LMAX];
-        float4 fpa[LMAX];
-        int2 fpg[LMAX];
 #pragma unroll
         for (int l = 0; l < LMAX; ++l) {
             const int lc = min(l, L - 1);
             const int s = lc * a.P + pc;
             load_sample_raw(ob + s * 2 * ka.osz, abase + s * ka.asz, ka.osz, ka.asz, o0[l], o1[l], at[l]);
-            const FineParams *f = fp_b + lc;
-            fpa[l] = *reinterpret_cast<const float4 *>(f);
-            fpg[l] = *reinterpret_cast<const int2 *>(&f->gx);
         }
         // ---- sample locations and every level's cell entry
         float sxl[LMAX], syl[LMAX];
         int2 ce[LMAX];
         bool inside[LMAX];
+        auto locate = [&](const FineParams *fpb) {
 #pragma unroll
-        for (int l = 0; l < LMAX; ++l) {
+            for (int l = 0; l < LMAX; ++l) {
 #pragma clang fp contract(off)
-            const int lc = min(l, L - 1);
-            sxl[l] = qx + raw_to_float(o0[l], a.off_dtype);
-            syl[l] = qy + raw_to_float(a.off_dtype == AFF_F32 ? o1[l] : o0[l] >> 16, a.off_dtype);
-            const float fx = floorf(__fmul_rn(__fsub_rn(sxl[l], fpa[l].x), fpa[l].w));
-            const float fy = floorf(__fmul_rn(__fsub_rn(syl[l], fpa[l].y), fpa[l].w));
-            inside[l] = fx >= 0.f && fx < float(fpg[l].x) && fy >= 0.f && fy < float(fpg[l].y);
-            const int cell = inside[l] ? int(fy) * fpg[l].x + int(fx) : 0;
-            ce[l] = fc_b[ka.fc_off[lc] + cell];
-        }
+                const int lc = min(l, L - 1);
+                const FineParams f = fpb[lc];
+                sxl[l] = qx + raw_to_float(o0[l], a.off_dtype);
+                syl[l] = qy + raw_to_float(a.off_dtype == AFF_F32 ? o1[l] : o0[l] >> 16, a.off_dtype);
+                const float fx = floorf(__fmul_rn(__fsub_rn(sxl[l], f.x0), f.inv_s));
+                const float fy = floorf(__fmul_rn(__fsub_rn(syl[l], f.y0), f.inv_s));
+                inside[l] = fx >= 0.f && fx < float(f.gx) && fy >= 0.f && fy < float(f.gy);
+                const int cell = inside[l] ? int(fy) * f.gx + int(fx) : 0;
+                ce[l] = fc_b[ka.fc_off[lc] + cell];
+            }
+        };
+        if (uni) locate(ka.fp + b0 * L);
+        else locate(ka.fp + b * L);
 
         // Levels in turn: level l's values sit at index 0 of the staged arrays,
         // which shift down by one after each level (constant indices keep
@@ -497,24 +538,54 @@ __global__ __launch_bounds__(THREADS) void deform_cand_kernel(const CArgs ka) {
             uint64_t keys[KT];
 #pragma unroll
             for (int j = 0; j < KT; ++j) keys[j] = ~0ull;
-            const int cnt = act && keff > 0 ? (inside[0] ? ce[0].y : -1) : 0;
+            const int cy_raw = act && keff > 0 ? (inside[0] ? ce[0].y : -1) : 0;
+            const int cnt = cy_raw > 0 ? cy_raw & 0xffff : cy_raw, head = cy_raw > 0 ? cy_raw >> 16 : 0;
             if (cnt > 0) {
-                // Four entries per step, the next four loaded during this step.
-                // Lanes past their list's end all read the pool's first entry:
-                // one L1 access between them instead of one each.
+                // Lists are padded to whole 4-entry steps (points at infinity) and the
+                // next step's entries are loaded during this one (past a list's end
+                // they are other lists' entries, or the pool's slack, and unused).
+                // Within the sorted head a lane stops once the next entry's distance
+                // to the cell exceeds its K-th distance: the head is sorted by that
+                // distance, computed here exactly as the build computed it (same
+                // widened rectangle, no contraction), so it bounds the entry and
+                // every later one from below (scaled down a little against the
+                // rounding of either distance).  An unfilled K-th key reads as NaN,
+                // which never compares less.
+                FineParams f;
+                if (uni) f = ka.fp[b0 * L + l];
+                else f = ka.fp[b * L + l];
+                Rect rc;
+                {
+#pragma clang fp contract(off)
+                    const int cx = int(floorf(__fmul_rn(__fsub_rn(sx, f.x0), f.inv_s)));
+                    const int cy = int(floorf(__fmul_rn(__fsub_rn(sy, f.y0), f.inv_s)));
+                    rc = fine_rect(f, cy * f.gx + cx);
+                }
+                auto below = [&](const Cand &e) {
+#pragma clang fp contract(off)
+                    const float dx = fmaxf(0.f, fmaxf(rc.x0 - e.x, e.x - rc.x1));
+                    const float dy = fmaxf(0.f, fmaxf(rc.y0 - e.y, e.y - rc.y1));
+                    return (dx * dx + dy * dy) * 0.999996f > key_d2(keys[KT - 1]);
+                };
                 const Cand *cp = ka.pool + b * ka.pool_per_b + ce[0].x;
-                Cand c4[4];
+                const bool can_stop = keff == KT;
+                Cand ca[4], cb[4];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) c4[u] = u < cnt ? cp[u] : ka.pool[0];
-                for (int i = 0; i < cnt; i += 4) {
-                    Cand n4[4];
+                for (int u = 0; u < 4; ++u) ca[u] = cp[u];
+                for (int i = 0;; i += 8) {
+                    if (can_stop && i < head && below(ca[0])) break;
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) n4[u] = i + 4 + u < cnt ? cp[i + 4 + u] : ka.pool[0];
+                    for (int u = 0; u < 4; ++u) cb[u] = cp[i + 4 + u];
 #pragma unroll
                     for (int u = 0; u < 4; ++u)
-                        if (i + u < cnt) topk_insert<KT>(keys, make_key(dist2(c4[u].x, c4[u].y, sx, sy), c4[u].row));
+                        topk_insert<KT>(keys, make_key(dist2(ca[u].x, ca[u].y, sx, sy), ca[u].row));
+                    if (i + 4 >= cnt || (can_stop && i + 4 < head && below(cb[0]))) break;
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) c4[u] = n4[u];
+                    for (int u = 0; u < 4; ++u) ca[u] = cp[i + 8 + u];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        topk_insert<KT>(keys, make_key(dist2(cb[u].x, cb[u].y, sx, sy), cb[u].row));
+                    if (i + 8 >= cnt) break;
                 }
             } else if (cnt < 0) {
                 const SegView g = seg_view(ka.ws, ka.wl, ka.segs, b, l);
@@ -820,7 +891,7 @@ aff_status launch_deform_k(const aff_deform_args &a, const Segs &segs, const DLa
     ba.ws = ws;
     ba.fp = reinterpret_cast<FineParams *>(w + dl.fparams);
     ba.fcell = reinterpret_cast<int2 *>(w + dl.fcell);
-    ba.tsum = reinterpret_cast<int *>(w + dl.tsum);
+    ba.counter = reinterpret_cast<int *>(w + dl.counter);
     ba.pool = reinterpret_cast<Cand *>(w + dl.pool);
     for (int l = 0; l <= segs.L; ++l) {
         ba.fc_off[l] = dl.fc_off[l];
@@ -831,9 +902,9 @@ aff_status launch_deform_k(const aff_deform_args &a, const Segs &segs, const DLa
     ba.pool_per_b = dl.pool_per_b;
     ba.tt_per_b = dl.tt_per_b;
     ba.K = a.K;
-    const unsigned nbuild = (unsigned)(a.B * dl.tt_per_b);
-    hipLaunchKernelGGL((cand_count_kernel<KT>), dim3(nbuild), dim3(CB), 0, s, ba);
-    hipLaunchKernelGGL((cand_fill_kernel<KT>), dim3(nbuild), dim3(CB), 0, s, ba);
+    const aff_status st = grid::launch_build(a.kv_pos, a.kp_sb, a.kp_sn, a.B, segs, ws, s, ZeroSpan{ba.counter, a.B});
+    if (st != AFF_OK) return st;
+    hipLaunchKernelGGL((cand_build_kernel<KT>), dim3((unsigned)(a.B * dl.tt_per_b)), dim3(CB), 0, s, ba);
 
     CArgs ka{};
     ka.a = a;
@@ -963,8 +1034,6 @@ extern "C" aff_status aff_deform_fwd(const aff_deform_args *args, void *ws, size
     AFF_CHECK_ARG((reinterpret_cast<uintptr_t>(ws) & 255) == 0, "aff_deform_fwd: workspace must be 256-byte aligned");
     AFF_CHECK_ARG((int64_t)a.B * dl.tt_per_b < ((int64_t)1 << 31), "aff_deform_fwd: too many build tiles");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    st = grid::launch_build(a.kv_pos, a.kp_sb, a.kp_sn, a.B, segs, ws, s);
-    if (st != AFF_OK) return st;
     if (a.dtype == AFF_F32) return deform::launch_deform<float>(a, segs, dl, ws, s);
     if (a.dtype == AFF_BF16) return deform::launch_deform<bf16_t>(a, segs, dl, ws, s);
     return deform::launch_deform<f16_t>(a, segs, dl, ws, s);

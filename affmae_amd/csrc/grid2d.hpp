@@ -101,12 +101,21 @@ struct QueryBin {
     float4 *out;
 };
 
+// Optional: ints the build sets to zero before anything that runs after it on
+// the stream (allocation counters of later passes).
+struct ZeroSpan {
+    int *p;
+    int n;
+};
+
 // Builds the grids of all B * s.L segments (defined in knn.hip).
 // src: point (b, row) at src[b * sb + row * sn + {0, 1}], rows as in s.start.
 aff_status launch_build(const float *src, int64_t sb, int64_t sn, int B, const Segs &s, void *ws,
                         hipStream_t stream);
 aff_status launch_build(const float *src, int64_t sb, int64_t sn, int B, const Segs &s, void *ws,
                         hipStream_t stream, const QueryBin &qb);
+aff_status launch_build(const float *src, int64_t sb, int64_t sn, int B, const Segs &s, void *ws,
+                        hipStream_t stream, const ZeroSpan &z);
 
 // Cell coordinate of v along one axis.  Monotone non-decreasing in v, which
 // is what makes "all points with coordinate in [a, b] lie in cells

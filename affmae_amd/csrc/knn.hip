@@ -89,7 +89,7 @@ __device__ void block_exclusive_scan(int *s_cnt, int n, int *s_wave, int *gout) 
 // cell tile into qb.out[b * M + slot] = (x, y, query index bits, 0).
 __global__ __launch_bounds__(BUILD_THREADS) void grid_build_kernel(const float *__restrict__ src, int64_t sb,
                                                                    int64_t sn, const Segs s, void *ws, WsLayout L,
-                                                                   QueryBin qb) {
+                                                                   QueryBin qb, ZeroSpan z) {
     __shared__ int s_cnt[MAX_CELLS];
     __shared__ float s_red[4][BUILD_THREADS / 64];
     __shared__ int s_wave[BUILD_THREADS / 64];
@@ -98,6 +98,8 @@ __global__ __launch_bounds__(BUILD_THREADS) void grid_build_kernel(const float *
     const int seg = blockIdx.x;
     const int b = seg / s.L, l = seg % s.L;
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    if (seg == 0)
+        for (int i = tid; i < z.n; i += BUILD_THREADS) z.p[i] = 0;
     constexpr int NW = BUILD_THREADS / 64;
     const int n = s.start[l + 1] - s.start[l];
     const int cmax = s.cmax[l];
@@ -252,11 +254,22 @@ __global__ __launch_bounds__(BUILD_THREADS) void grid_build_kernel(const float *
     }
 }
 
+static aff_status launch_build_impl(const float *src, int64_t sb, int64_t sn, int B, const Segs &s, void *ws,
+                                    hipStream_t stream, const QueryBin &qb, const ZeroSpan &z) {
+    const WsLayout L = ws_layout(B, s);
+    hipLaunchKernelGGL(grid_build_kernel, dim3(B * s.L), dim3(BUILD_THREADS), 0, stream, src, sb, sn, s, ws, L, qb,
+                       z);
+    return check_launch("grid_build");
+}
+
 aff_status launch_build(const float *src, int64_t sb, int64_t sn, int B, const Segs &s, void *ws,
                         hipStream_t stream, const QueryBin &qb) {
-    const WsLayout L = ws_layout(B, s);
-    hipLaunchKernelGGL(grid_build_kernel, dim3(B * s.L), dim3(BUILD_THREADS), 0, stream, src, sb, sn, s, ws, L, qb);
-    return check_launch("grid_build");
+    return launch_build_impl(src, sb, sn, B, s, ws, stream, qb, ZeroSpan{nullptr, 0});
+}
+
+aff_status launch_build(const float *src, int64_t sb, int64_t sn, int B, const Segs &s, void *ws,
+                        hipStream_t stream, const ZeroSpan &z) {
+    return launch_build_impl(src, sb, sn, B, s, ws, stream, QueryBin{nullptr, 0, 0, 0, nullptr}, z);
 }
 
 aff_status launch_build(const float *src, int64_t sb, int64_t sn, int B, const Segs &s, void *ws,
