@@ -36,7 +36,7 @@ using namespace grid;
 constexpr int THREADS = 256;
 constexpr int KMAX = 8;    // neighbours per sample
 constexpr int NB = 8;      // value rows in flight per lane (given-index kernels)
-constexpr int PAIR_GROUP = 16;  // the deformable gather's rows in flight per lane; pair lists pad to a multiple
+constexpr int PAIR_GROUP = 8;   // the deformable gather's rows in flight per lane; pair lists pad to a multiple
 
 // Fine-cell candidate lists.  Every (image, level) gets a second, finer grid
 // (cells of FINE x FINE per coarse cell, FPAD coarse cells of margin around
@@ -594,8 +594,12 @@ __global__ __launch_bounds__(THREADS) void deform_cand_kernel(const CArgs ka) {
                 const float U0 = keff >= g.n ? INFINITY : fmaxf(float(keff + 4) / (3.14159265f * rho), 1e-30f);
                 topk_global<KT>(g, sx, sy, U0, keff, keys);
             }
-            if (act) {
-                const float aw = raw_to_float(at[0], a.attn_dtype);
+            // ---- this sample's neighbours: value offsets and weights (none for
+            // inactive lanes)
+            int nb[KT];
+            float wt[KT];
+            {
+                const float aw = act ? raw_to_float(at[0], a.attn_dtype) : 0.f;
                 float wj[KT];
                 float wsum = 0.f;
                 if (a.mode == AFF_DEFORM_SHEPARD) {
@@ -631,24 +635,27 @@ __global__ __launch_bounds__(THREADS) void deform_cand_kernel(const CArgs ka) {
                     wsum += 1e-12f;
                 }
                 const float inv = __builtin_amdgcn_rcpf(wsum);
+#pragma unroll
+                for (int j = 0; j < KT; ++j) {
+                    const bool ok = act && j < keff && j < K;
+                    nb[j] = ok ? key_index(keys[j]) * int(a.v_sn) + vrow : -1;
+                    wt[j] = ok ? aw * wj[j] * inv : 0.f;
+                }
+            }
+            if (act) {
                 int2 *dst = pr + r * SKP + s * K;
+#pragma unroll
+                for (int j = 0; j < KT; ++j)
+                    if (j < K) dst[j] = make_int2(nb[j] >= 0 ? nb[j] : vrow, __float_as_int(wt[j]));
+            }
+            if (act && (a.knn_idx || a.knn_d2)) {
+                const int64_t kb = (row * S + s) * K;  // [B, Nq, H, L, P, K]
 #pragma unroll
                 for (int j = 0; j < KT; ++j) {
                     if (j < K) {
                         const bool ok = j < keff;
-                        dst[j] = make_int2(ok ? key_index(keys[j]) * int(a.v_sn) + vrow : vrow,
-                                           __float_as_int(ok ? aw * wj[j] * inv : 0.f));
-                    }
-                }
-                if (a.knn_idx || a.knn_d2) {
-                    const int64_t kb = (row * S + s) * K;  // [B, Nq, H, L, P, K]
-#pragma unroll
-                    for (int j = 0; j < KT; ++j) {
-                        if (j < K) {
-                            const bool ok = j < keff;
-                            if (a.knn_idx) a.knn_idx[kb + j] = ok ? key_index(keys[j]) - lstart : -1;
-                            if (a.knn_d2) a.knn_d2[kb + j] = ok ? key_d2(keys[j]) : INFINITY;
-                        }
+                        if (a.knn_idx) a.knn_idx[kb + j] = ok ? key_index(keys[j]) - lstart : -1;
+                        if (a.knn_d2) a.knn_d2[kb + j] = ok ? key_d2(keys[j]) : INFINITY;
                     }
                 }
             }
@@ -666,10 +673,10 @@ __global__ __launch_bounds__(THREADS) void deform_cand_kernel(const CArgs ka) {
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // ---- gather: pairs (value offset of (row, head) in elements, weight), padded
-    // to SKP with weight-0 pairs; GB rows in flight per lane, pairs read two per
-    // LDS access
-    constexpr int GB = sizeof(T) == 2 ? PAIR_GROUP : PAIR_GROUP / 2;
+    // ---- gather: each row's SKP pairs (value offset of (row, head) in elements,
+    // weight; the padding has weight 0); GB rows in flight per lane, pairs read
+    // two per LDS access
+    constexpr int GB = PAIR_GROUP;
     const int CG = a.C / 8;
     for (int it = lane; it < RW * CG; it += 64) {
         const int rr = it / CG, cc = it - rr * CG;
