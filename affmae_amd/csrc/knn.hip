@@ -490,6 +490,7 @@ __global__ __launch_bounds__(WIN_THREADS) void knn_win_kernel(const float4 *__re
     __shared__ int s_wcs[WC];
     __shared__ int s_rb[WROWS + 1];
     __shared__ int s_gb[WROWS];
+    __shared__ uint8_t s_rowof[WM];  // window row of each window point slot
     __shared__ uint32_t s_list[(CAP / 2 + 1) * WIN_THREADS];  // CAP entries + 2 spare entries per lane
 
     const int lane = threadIdx.x;
@@ -541,6 +542,7 @@ __global__ __launch_bounds__(WIN_THREADS) void knn_win_kernel(const float4 *__re
             if (lane < WY) {
                 s_rb[lane] = incl - cnt;
                 s_gb[lane] = gb;
+                for (int j = incl - cnt; j < incl; ++j) s_rowof[j] = uint8_t(lane);  // this row's slots
             }
             if (lane == 0) s_rb[WY] = total;
             __syncthreads();
@@ -549,8 +551,7 @@ __global__ __launch_bounds__(WIN_THREADS) void knn_win_kernel(const float4 *__re
                 s_wcs[e] = s_rb[r] + g.cs[(wy0 + r) * p.gx + wx0 + c] - s_gb[r];
             }
             for (int t = lane; t < total; t += WIN_THREADS) {
-                int r = 0;
-                while (s_rb[r + 1] <= t) ++r;
+                const int r = s_rowof[t];
                 const float4 pt = g.P[s_gb[r] + (t - s_rb[r])];
                 s_xy[t] = make_float2(pt.x, pt.y);
                 s_id[t] = uint16_t(__float_as_int(pt.z));
