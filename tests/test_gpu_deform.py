@@ -172,6 +172,30 @@ def test_neighbour_search_edge_cases(oracle_mod, dev, name, K, off_sd):
     _close(out, ro, torch.float32)
 
 
+@pytest.mark.parametrize("L,P,K,dtype", [(8, 1, 5, torch.float32), (3, 3, 2, torch.float16), (1, 8, 8, torch.float32),
+                                          (2, 16, 1, torch.bfloat16), (4, 4, 3, torch.float16)])
+def test_level_point_neighbour_shapes(oracle_mod, dev, L, P, K, dtype):
+    """Shapes off the cfg4 path: up to 8 levels, 1..16 points per level (1..16 lanes per
+    row), K below the register slot count (no early stop), fp16 / bf16 / fp32 values."""
+    print(f"[deform shapes] L={L} P={P} K={K} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(17 + L * 7 + P)
+    B, Nq, H, C = 2, 160, 3, 16
+    sizes = [max(K, 300 >> l) for l in range(L)]
+    kv = torch.cat([torch.rand((B, n, 2), generator=g) for n in sizes], dim=1)
+    ls = [0]
+    for n in sizes:
+        ls.append(ls[-1] + n)
+    qp = torch.rand((B, Nq, 2), generator=g)
+    off = (torch.randn((B, Nq, H, L, P, 2), generator=g) * 0.04).to(dtype)
+    att = torch.softmax(torch.randn((B, Nq, H, L * P), generator=g), -1).reshape(B, Nq, H, L, P).to(dtype)
+    val = torch.randn((B, ls[-1], H, C), generator=g).to(dtype)
+    out, ki, _ = ms_deformable_attention(qp.to(dev), kv.to(dev), ls, off.to(dev), att.to(dev), val.to(dev),
+                                         power=2.0, k=K, weighting="idw", return_knn=True)
+    ro, ri = oracle_mod.deform(qp.numpy(), kv.numpy(), ls, _np(off), _np(att), _np(val), 2.0, K, "idw")
+    np.testing.assert_array_equal(ki.cpu().numpy(), ri)
+    _close(out, ro, dtype)
+
+
 def test_given_index_kernels(oracle_mod, dev):
     g = torch.Generator().manual_seed(4)
     B, N, Nkv, K, C = 2, 300, 400, 4, 24
