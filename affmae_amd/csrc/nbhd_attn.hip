@@ -917,66 +917,77 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
         nmask += (live && !ok) ? 1 : 0;
     }
 
-    // ---- biases of the entries, every head, times log2(e), for bm.  The usual case
-    // (fp32 table, 4 heads) keeps the table rows in flight in registers until the
-    // union is built; the others store at once.
+    // ---- biases of the entries, every head, times log2(e), for bm.  Table modes
+    // (2, 4): the entries' table-row inputs (pe rows, or the neighbours' coordinates)
+    // are loaded here and stay in flight through the union steps; the rows are read
+    // and bm written after the slots (write_table_biases).  Modes 1 and 3 store at
+    // once; mode 0 stores zeros.
     const int rowq_b = 2 * H + q * M * H;  // bm word of (q, j = 0, h = 0)
     const bool fast4 = (BIAS == 2 || BIAS == 4) && H == 4 && a.table_dtype == AFF_F32;
-    float4 tv[RJ];
-    bool tin[RJ];
+    float2 gq[RJ];   // BIAS 4: neighbour coordinates
+    int64_t prow[RJ];  // BIAS 2: pe rows
+    float pqx = 0.f, pqy = 0.f;
+    const float *pos_b = nullptr;
+    if constexpr (BIAS == 3 || BIAS == 4) {
+        pos_b = a.pos + (int64_t)b * a.pos_sb;
+        const float2 pq = *reinterpret_cast<const float2 *>(pos_b + (int64_t)nc * a.pos_sn);
+        pqx = pq.x;
+        pqy = pq.y;
+    }
+    const int Tw = 2 * a.rel_width + 1;
 #pragma unroll
     for (int r = 0; r < RJ; ++r) {
-        tv[r] = make_float4(0.f, 0.f, 0.f, 0.f);
-        tin[r] = false;
-    }
-    if constexpr (BIAS != 0) {
-        float pqx = 0.f, pqy = 0.f;
-        const float *pos_b = nullptr;
-        if constexpr (BIAS == 3 || BIAS == 4) {
-            pos_b = a.pos + (int64_t)b * a.pos_sb;
-            const float2 pq = *reinterpret_cast<const float2 *>(pos_b + (int64_t)nc * a.pos_sn);
-            pqx = pq.x;
-            pqy = pq.y;
-        }
-        const int Tw = 2 * a.rel_width + 1;
-#pragma unroll
-        for (int r = 0; r < RJ; ++r) {
-            if (r >= nr || !use[r]) continue;
-            const int j = jl + LPQ * r;
-            float *dst = bm + rowq_b + j * H;
-            int64_t row = -1;
-            if constexpr (BIAS == 2) {
+        gq[r] = make_float2(0.f, 0.f);
+        prow[r] = -1;
+        if (r >= nr) continue;
+        const int j = jl + LPQ * r;
+        if constexpr (BIAS == 4) {
+            gq[r] = *reinterpret_cast<const float2 *>(pos_b + (int64_t)idx[r] * a.pos_sn);  // idx[r] is a valid row
+        } else if constexpr (BIAS == 2) {
+            if (use[r]) {
                 const int64_t e = (int64_t)b * a.pe_sb + (int64_t)nc * a.pe_sn + j;
-                row = a.pe_is_i64 ? static_cast<const int64_t *>(a.pe_idx)[e]
-                                  : int64_t(static_cast<const int32_t *>(a.pe_idx)[e]);
-            } else if constexpr (BIAS == 4) {
-                const float2 g = *reinterpret_cast<const float2 *>(pos_b + (int64_t)idx[r] * a.pos_sn);
-                row = pe_from_coords32(pqx, pqy, g.x, g.y, float(a.rel_width), float(Tw));
+                prow[r] = a.pe_is_i64 ? static_cast<const int64_t *>(a.pe_idx)[e]
+                                      : int64_t(static_cast<const int32_t *>(a.pe_idx)[e]);
             }
-            if constexpr (BIAS == 2 || BIAS == 4) {
-                const bool in = row >= 0 && row < a.table_rows;
-                if (fast4) {
-                    tin[r] = in;
-                    tv[r] = reinterpret_cast<const float4 *>(a.table)[in ? row : 0];
-                } else {
-                    for (int h = 0; h < H; ++h)
-                        dst[h] = in ? load_any(a.table, a.table_dtype, row * H + h) * LOG2E : 0.f;
-                }
-            } else if constexpr (BIAS == 1) {
+        } else if constexpr (BIAS == 1) {
+            if (use[r]) {
+                float *dst = bm + rowq_b + j * H;
                 const int64_t e = (int64_t)b * a.bias_sb + (int64_t)nc * a.bias_sn + j;
                 for (int h = 0; h < H; ++h) dst[h] = load_any(a.bias, a.bias_dtype, e + (int64_t)h * a.bias_sh) * LOG2E;
-            } else if constexpr (BIAS == 3) {
+            }
+        } else if constexpr (BIAS == 3) {
+            if (use[r]) {
+                float *dst = bm + rowq_b + j * H;
                 const float2 g = *reinterpret_cast<const float2 *>(pos_b + (int64_t)idx[r] * a.pos_sn);
                 for (int h = 0; h < H; ++h) dst[h] = cont_bias(a.pos_w + h * 5, a.pos_b[h], g.x - pqx, g.y - pqy) * LOG2E;
             }
+        } else {
+            // no bias: zero entries, so that every (query, neighbour) pair still has its own code
+            if (use[r])
+                for (int h = 0; h < H; ++h) bm[rowq_b + j * H + h] = 0.f;
         }
-    } else {
-        // no bias: zero entries, so that every (query, neighbour) pair still has its own code
-#pragma unroll
-        for (int r = 0; r < RJ; ++r)
-            if (r < nr && use[r])
-                for (int h = 0; h < H; ++h) bm[rowq_b + (jl + LPQ * r) * H + h] = 0.f;
     }
+    auto write_table_biases = [&]() {
+        if constexpr (BIAS == 2 || BIAS == 4) {
+#pragma unroll
+            for (int r = 0; r < RJ; ++r) {
+                if (r >= nr || !use[r]) continue;
+                const int j = jl + LPQ * r;
+                int64_t row;
+                if constexpr (BIAS == 2) row = prow[r];
+                else row = pe_from_coords32(pqx, pqy, gq[r].x, gq[r].y, float(a.rel_width), float(Tw));
+                const bool in = row >= 0 && row < a.table_rows;
+                float *dst = bm + rowq_b + j * H;
+                if (fast4) {
+                    const float4 tv = reinterpret_cast<const float4 *>(a.table)[in ? row : 0];
+                    const float sc = in ? LOG2E : 0.f;
+                    *reinterpret_cast<float4 *>(dst) = make_float4(tv.x * sc, tv.y * sc, tv.z * sc, tv.w * sc);
+                } else {
+                    for (int h = 0; h < H; ++h) dst[h] = in ? load_any(a.table, a.table_dtype, row * H + h) * LOG2E : 0.f;
+                }
+            }
+        }
+    };
     // the cleared flags are visible before any wave sets one (the loads above stay
     // in flight across this barrier)
     lds_barrier();
@@ -1000,7 +1011,7 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
     }
     lds_barrier();
 
-    // ---- flags -> bits (thread t packs window word t); the biases held in registers -> bm
+    // ---- flags -> bits (thread t packs window word t)
     {
         const uint4 f0 = reinterpret_cast<const uint4 *>(sh.s.flg)[2 * t];
         const uint4 f1 = reinterpret_cast<const uint4 *>(sh.s.flg)[2 * t + 1];
@@ -1009,15 +1020,6 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
 #pragma unroll
         for (int k = 0; k < 8; ++k) wbits |= (((d[k] * 0x01020408u) >> 24) & 0xFu) << (4 * k);  // 4 flag bytes -> 4 bits
         sh.s.bits[t] = wbits;
-    }
-    if (fast4) {
-#pragma unroll
-        for (int r = 0; r < RJ; ++r)
-            if (r < nr && use[r]) {
-                const float sc = tin[r] ? LOG2E : 0.f;
-                *reinterpret_cast<float4 *>(bm + rowq_b + (jl + LPQ * r) * 4) =
-                    make_float4(tv[r].x * sc, tv[r].y * sc, tv[r].z * sc, tv[r].w * sc);
-            }
     }
     lds_barrier();
 
@@ -1065,6 +1067,7 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
                 pw[rowq + s_] = uint16_t(uint32_t(rowq_b + (jl + LPQ * r) * H) * 4);
             }
         }
+        write_table_biases();
     }
     lds_barrier();
     if (!fallback) {
