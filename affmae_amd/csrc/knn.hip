@@ -29,6 +29,8 @@
 
 #include <limits.h>
 
+#include <mutex>
+
 namespace aff {
 namespace grid {
 
@@ -480,11 +482,61 @@ __device__ __forceinline__ int radius_select(Visit &&visit, float U, int k, uint
     return -1;
 }
 
+// The first k sorted keys of the wave's queries, written row by row: the keys
+// go through LDS (buf: (CAP / 2 + 1) words per lane) in column chunks of CAP / 2,
+// and each store instruction then covers consecutive words of a few output rows
+// instead of one word in each of 64 rows.  qrow[r] is the output row of lane r;
+// rows r >= nq are not written.  Called by the whole wave.
+template <int CAP>
+__device__ __forceinline__ void store_rows_wave(const uint64_t (&a)[CAP], int k, int nq, const int *qrow,
+                                                uint32_t *buf, int lane, void *out_idx, int idx_i64, float *out_d2,
+                                                int64_t row0) {
+    constexpr int CW = CAP / 2, SP = CW + 1;
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+        if (pass == 1 && !out_d2) break;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int c0 = h * CW;
+            if (c0 >= k) break;
+            const int cols = min(CW, k - c0);
+            __syncthreads();  // the buffer's previous readers are done
+#pragma unroll
+            for (int j = 0; j < CW; ++j)
+                if (j < cols) buf[lane * SP + j] = pass ? uint32_t(a[c0 + j] >> 32) : uint32_t(a[c0 + j]);
+            __syncthreads();
+            const int rpi = WIN_THREADS / cols;  // rows per store instruction
+            const int rr = lane / cols, c = lane - rr * cols;
+            // eight store instructions per step, their LDS reads issued together
+            for (int r0 = 0; r0 < nq; r0 += 8 * rpi) {
+                uint32_t v[8];
+                int64_t o[8];
+                bool ok[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int r = r0 + u * rpi + rr;
+                    ok[u] = rr < rpi && r < nq;
+                    const int rc = ok[u] ? r : 0;
+                    v[u] = buf[rc * SP + c];
+                    o[u] = (row0 + qrow[rc]) * k + c0 + c;
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    if (!ok[u]) continue;
+                    if (pass) out_d2[o[u]] = __uint_as_float(v[u]);
+                    else if (idx_i64) static_cast<int64_t *>(out_idx)[o[u]] = int32_t(v[u]);
+                    else static_cast<int32_t *>(out_idx)[o[u]] = int32_t(v[u]);
+                }
+            }
+        }
+    }
+}
+
 template <int CAP, int WM, int WC>
 __global__ __launch_bounds__(WIN_THREADS) void knn_win_kernel(const float4 *__restrict__ qsorted, const Segs s,
                                                               const void *ws, WsLayout L, int M, int k,
                                                               void *__restrict__ out_idx, int idx_i64,
-                                                              float *__restrict__ out_d2) {
+                                                              float *__restrict__ out_d2, int row_store) {
     __shared__ float2 s_xy[WM + 3];  // + spare entries read (and ignored) by the 4-wide visits
     __shared__ uint16_t s_id[WM];  // point indices (the windowed path takes N <= 65536)
     __shared__ int s_wcs[WC];
@@ -602,9 +654,7 @@ __global__ __launch_bounds__(WIN_THREADS) void knn_win_kernel(const float4 *__re
             cnt = k;
         }
     }
-    if (!active) return;
-
-    // ---- keys, sort, first k out
+    // ---- keys, sort, first k out (inactive lanes carry keys ~0 and write nothing)
     // (loads fenced in groups of 8 so the scheduler does not hoist all of them
     // and raise the register count past two waves per SIMD)
     uint64_t a[CAP];
@@ -632,8 +682,33 @@ __global__ __launch_bounds__(WIN_THREADS) void knn_win_kernel(const float4 *__re
     }
     __builtin_amdgcn_sched_barrier(0);
     sort_keys<CAP>(a);
-    const int64_t obase = ((int64_t)b * M + qi) * k;
-    store_row<CAP>(a, k, out_idx, idx_i64, out_d2, obase);
+    if (row_store) {
+        s_gb[lane] = qi;  // the window's row bases are dead: output row of each lane's query
+        store_rows_wave<CAP>(a, k, min(WIN_THREADS, M - (int)blockIdx.x * WIN_THREADS), s_gb, s_list, lane, out_idx,
+                             idx_i64, out_d2, (int64_t)b * M);
+    } else if (active) {
+        store_row<CAP>(a, k, out_idx, idx_i64, out_d2, ((int64_t)b * M + qi) * k);
+    }
+}
+
+// Workgroups of a windowed kernel resident on one CU, queried once per kernel.
+static int win_resident_per_cu(const void *fn) {
+    constexpr int SLOTS = 8;
+    static const void *keys[SLOTS];
+    static int vals[SLOTS];
+    static std::mutex mu;
+    std::lock_guard<std::mutex> lock(mu);
+    for (int i = 0; i < SLOTS; ++i)
+        if (keys[i] == fn) return vals[i];
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, WIN_THREADS, 0) != hipSuccess || n <= 0) n = 8;
+    for (int i = 0; i < SLOTS; ++i)
+        if (!keys[i]) {
+            keys[i] = fn;
+            vals[i] = n;
+            break;
+        }
+    return n;
 }
 
 }  // namespace knn
@@ -686,7 +761,7 @@ extern "C" aff_status aff_knn(const float *query, int64_t q_sb, int64_t q_sm, co
         // sparser queries spread a wave's 64 queries over more points: take the wider window
         const bool wide = 2 * (int64_t)M < (int64_t)N;
         using WinFn = void (*)(const float4 *, const grid::Segs, const void *, grid::WsLayout, int, int, void *, int,
-                               float *);
+                               float *, int);
         WinFn fn;
         if (k <= 12)
             fn = wide ? knn::knn_win_kernel<16, knn::WMAX_WIDE, knn::WCMAX_WIDE>
@@ -697,7 +772,13 @@ extern "C" aff_status aff_knn(const float *query, int64_t q_sb, int64_t q_sm, co
         else
             fn = wide ? knn::knn_win_kernel<64, knn::WMAX_WIDE, knn::WCMAX_WIDE>
                       : knn::knn_win_kernel<64, knn::WMAX, knn::WCMAX>;
-        hipLaunchKernelGGL(fn, gridd, block, 0, st, qsorted, s, ws, L, M, k, out_idx, idx_is_i64, out_d2);
+        // More waves than fit at once: the launch is throughput bound, and whole-row
+        // stores (through LDS) cost the memory path far less than one word per row per
+        // store.  One resident generation: the direct stores end each wave sooner.
+        const int64_t waves = (int64_t)gridd.x * gridd.y;
+        const int row_store =
+            waves > (int64_t)knn::win_resident_per_cu(reinterpret_cast<const void *>(fn)) * device_cu_count();
+        hipLaunchKernelGGL(fn, gridd, block, 0, st, qsorted, s, ws, L, M, k, out_idx, idx_is_i64, out_d2, row_store);
     } else if (k <= 64) {
         hipLaunchKernelGGL(knn::knn_query_kernel<64>, gridd, block, 0, st, query, q_sb, q_sm, s, ws, L, M, k, out_idx,
                            idx_is_i64, out_d2);

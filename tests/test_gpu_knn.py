@@ -44,6 +44,16 @@ def test_cfg2_full_batch(oracle_mod, dev):
     _check(pos, pos, 48, oracle_mod, dev, out_dtype=torch.int32)
 
 
+@pytest.mark.parametrize("k,out_dtype", [(5, torch.int64), (13, torch.int32), (20, torch.int64),
+                                         (48, torch.int64), (64, torch.int32)])
+def test_more_waves_than_resident(oracle_mod, dev, k, out_dtype):
+    """40 images of 6272 points: more waves than the GPU holds at once, so the
+    windowed kernel writes whole output rows through LDS (every column-chunk
+    width: k below, at and above half the candidate cap)."""
+    pos = workloads.jittered_grid(40, 112, 6272, seed=k)
+    _check(pos, pos, k, oracle_mod, dev, out_dtype=out_dtype)
+
+
 def test_cfg3_cross(oracle_mod, dev):
     """Merged points (a seeded weighted subset) against all source tokens."""
     src = workloads.jittered_grid(4, 112, 6272, seed=0) / 112.0
