@@ -532,11 +532,11 @@ __device__ __forceinline__ void store_rows_wave(const uint64_t (&a)[CAP], int k,
     }
 }
 
-template <int CAP, int WM, int WC>
+template <int CAP, int WM, int WC, bool ROWS>
 __global__ __launch_bounds__(WIN_THREADS) void knn_win_kernel(const float4 *__restrict__ qsorted, const Segs s,
                                                               const void *ws, WsLayout L, int M, int k,
                                                               void *__restrict__ out_idx, int idx_i64,
-                                                              float *__restrict__ out_d2, int row_store) {
+                                                              float *__restrict__ out_d2) {
     __shared__ float2 s_xy[WM + 3];  // + spare entries read (and ignored) by the 4-wide visits
     __shared__ uint16_t s_id[WM];  // point indices (the windowed path takes N <= 65536)
     __shared__ int s_wcs[WC];
@@ -682,7 +682,7 @@ __global__ __launch_bounds__(WIN_THREADS) void knn_win_kernel(const float4 *__re
     }
     __builtin_amdgcn_sched_barrier(0);
     sort_keys<CAP>(a);
-    if (row_store) {
+    if constexpr (ROWS) {
         s_gb[lane] = qi;  // the window's row bases are dead: output row of each lane's query
         store_rows_wave<CAP>(a, k, min(WIN_THREADS, M - (int)blockIdx.x * WIN_THREADS), s_gb, s_list, lane, out_idx,
                              idx_i64, out_d2, (int64_t)b * M);
@@ -761,24 +761,32 @@ extern "C" aff_status aff_knn(const float *query, int64_t q_sb, int64_t q_sm, co
         // sparser queries spread a wave's 64 queries over more points: take the wider window
         const bool wide = 2 * (int64_t)M < (int64_t)N;
         using WinFn = void (*)(const float4 *, const grid::Segs, const void *, grid::WsLayout, int, int, void *, int,
-                               float *, int);
-        WinFn fn;
-        if (k <= 12)
-            fn = wide ? knn::knn_win_kernel<16, knn::WMAX_WIDE, knn::WCMAX_WIDE>
-                      : knn::knn_win_kernel<16, knn::WMAX, knn::WCMAX>;
-        else if (k <= 24)
-            fn = wide ? knn::knn_win_kernel<32, knn::WMAX_WIDE, knn::WCMAX_WIDE>
-                      : knn::knn_win_kernel<32, knn::WMAX, knn::WCMAX>;
-        else
-            fn = wide ? knn::knn_win_kernel<64, knn::WMAX_WIDE, knn::WCMAX_WIDE>
-                      : knn::knn_win_kernel<64, knn::WMAX, knn::WCMAX>;
+                               float *);
+        auto pick = [&](bool rows) -> WinFn {
+            if (k <= 12)
+                return wide ? (rows ? knn::knn_win_kernel<16, knn::WMAX_WIDE, knn::WCMAX_WIDE, true>
+                                    : knn::knn_win_kernel<16, knn::WMAX_WIDE, knn::WCMAX_WIDE, false>)
+                            : (rows ? knn::knn_win_kernel<16, knn::WMAX, knn::WCMAX, true>
+                                    : knn::knn_win_kernel<16, knn::WMAX, knn::WCMAX, false>);
+            if (k <= 24)
+                return wide ? (rows ? knn::knn_win_kernel<32, knn::WMAX_WIDE, knn::WCMAX_WIDE, true>
+                                    : knn::knn_win_kernel<32, knn::WMAX_WIDE, knn::WCMAX_WIDE, false>)
+                            : (rows ? knn::knn_win_kernel<32, knn::WMAX, knn::WCMAX, true>
+                                    : knn::knn_win_kernel<32, knn::WMAX, knn::WCMAX, false>);
+            return wide ? (rows ? knn::knn_win_kernel<64, knn::WMAX_WIDE, knn::WCMAX_WIDE, true>
+                                : knn::knn_win_kernel<64, knn::WMAX_WIDE, knn::WCMAX_WIDE, false>)
+                        : (rows ? knn::knn_win_kernel<64, knn::WMAX, knn::WCMAX, true>
+                                : knn::knn_win_kernel<64, knn::WMAX, knn::WCMAX, false>);
+        };
         // More waves than fit at once: the launch is throughput bound, and whole-row
         // stores (through LDS) cost the memory path far less than one word per row per
         // store.  One resident generation: the direct stores end each wave sooner.
+        const WinFn direct = pick(false);
         const int64_t waves = (int64_t)gridd.x * gridd.y;
-        const int row_store =
-            waves > (int64_t)knn::win_resident_per_cu(reinterpret_cast<const void *>(fn)) * device_cu_count();
-        hipLaunchKernelGGL(fn, gridd, block, 0, st, qsorted, s, ws, L, M, k, out_idx, idx_is_i64, out_d2, row_store);
+        const bool rows =
+            waves > (int64_t)knn::win_resident_per_cu(reinterpret_cast<const void *>(direct)) * device_cu_count();
+        hipLaunchKernelGGL(rows ? pick(true) : direct, gridd, block, 0, st, qsorted, s, ws, L, M, k, out_idx,
+                           idx_is_i64, out_d2);
     } else if (k <= 64) {
         hipLaunchKernelGGL(knn::knn_query_kernel<64>, gridd, block, 0, st, query, q_sb, q_sm, s, ws, L, M, k, out_idx,
                            idx_is_i64, out_d2);

@@ -967,22 +967,42 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
                 for (int h = 0; h < H; ++h) bm[rowq_b + j * H + h] = 0.f;
         }
     }
+    auto table_row = [&](int r) -> int64_t {
+        if constexpr (BIAS == 2) return prow[r];
+        else return pe_from_coords32(pqx, pqy, gq[r].x, gq[r].y, float(a.rel_width), float(Tw));
+    };
+    // fp32 table, 4 heads: one 16-byte row per entry, loaded after the bits step and
+    // stored to bm after the slots step
+    float4 tv[RJ];
+    float tsc[RJ];
+    auto load_table_rows = [&]() {
+        if constexpr (BIAS == 2 || BIAS == 4) {
+            if (fast4) {
+#pragma unroll
+                for (int r = 0; r < RJ; ++r) {
+                    tv[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    tsc[r] = 0.f;
+                    if (r >= nr || !use[r]) continue;
+                    const int64_t row = table_row(r);
+                    const bool in = row >= 0 && row < a.table_rows;
+                    tsc[r] = in ? LOG2E : 0.f;
+                    tv[r] = reinterpret_cast<const float4 *>(a.table)[in ? row : 0];
+                }
+            }
+        }
+    };
     auto write_table_biases = [&]() {
         if constexpr (BIAS == 2 || BIAS == 4) {
 #pragma unroll
             for (int r = 0; r < RJ; ++r) {
                 if (r >= nr || !use[r]) continue;
-                const int j = jl + LPQ * r;
-                int64_t row;
-                if constexpr (BIAS == 2) row = prow[r];
-                else row = pe_from_coords32(pqx, pqy, gq[r].x, gq[r].y, float(a.rel_width), float(Tw));
-                const bool in = row >= 0 && row < a.table_rows;
-                float *dst = bm + rowq_b + j * H;
+                float *dst = bm + rowq_b + (jl + LPQ * r) * H;
                 if (fast4) {
-                    const float4 tv = reinterpret_cast<const float4 *>(a.table)[in ? row : 0];
-                    const float sc = in ? LOG2E : 0.f;
-                    *reinterpret_cast<float4 *>(dst) = make_float4(tv.x * sc, tv.y * sc, tv.z * sc, tv.w * sc);
+                    const float sc = tsc[r];
+                    *reinterpret_cast<float4 *>(dst) = make_float4(tv[r].x * sc, tv[r].y * sc, tv[r].z * sc, tv[r].w * sc);
                 } else {
+                    const int64_t row = table_row(r);
+                    const bool in = row >= 0 && row < a.table_rows;
                     for (int h = 0; h < H; ++h) dst[h] = in ? load_any(a.table, a.table_dtype, row * H + h) * LOG2E : 0.f;
                 }
             }
@@ -1021,6 +1041,7 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
         for (int k = 0; k < 8; ++k) wbits |= (((d[k] * 0x01020408u) >> 24) & 0xFu) << (4 * k);  // 4 flag bytes -> 4 bits
         sh.s.bits[t] = wbits;
     }
+    load_table_rows();
     lds_barrier();
 
     const bool flagged = (a.mask && a.mask_sh != 0) || red[0] != 0;
