@@ -62,10 +62,18 @@ struct FineParams {
 // list starts with its HEAD points nearest to the cell sorted by that distance
 // (the head), so within the head the distance of an entry to the cell bounds
 // the distances of every later entry from below.
-struct Cand {
-    float x, y;
-    int row;
+// Entries are stored four to a block, fields apart, so that a scan step reads
+// a block as three 16-byte loads (lists start and end on block boundaries).
+struct alignas(16) CandBlock {
+    float x[4], y[4];
+    int row[4];
 };
+__device__ __forceinline__ void put_cand(CandBlock *blk, int slot, float x, float y, int row) {
+    CandBlock &c = blk[slot >> 2];
+    c.x[slot & 3] = x;
+    c.y[slot & 3] = y;
+    c.row[slot & 3] = row;
+}
 
 // Workspace of aff_deform_fwd: the coarse grids (grid2d.hpp), then the fine
 // grids' parameters, their (begin, count) cell tables, one pool allocation
@@ -108,8 +116,8 @@ inline DLayout d_layout(int B, const Segs &s, int K) {
     d.counter = off;
     off = align256(off + sizeof(int) * (size_t)B);
     d.pool_per_b = (int64_t)pool_per_point(K) * s.npts_b + 1024;
-    d.pool = off;  // + 4 entries: a scan's read-ahead past the last list stays inside
-    off = align256(off + sizeof(Cand) * ((size_t)B * (size_t)d.pool_per_b + 4));
+    d.pool = off;
+    off = align256(off + sizeof(CandBlock) * ((size_t)B * (size_t)d.pool_per_b / 4));
     d.total = off;
     return d;
 }
@@ -301,7 +309,7 @@ struct BArgs {
     FineParams *fp;  // [B * L]
     int2 *fcell;     // [B][fc_per_b]: (begin, count) of each fine cell's list
     int *counter;    // [B]: pool entries handed out per batch item
-    Cand *pool;      // [B][pool_per_b]
+    CandBlock *pool;  // [B][pool_per_b / 4]
     int fc_off[MAX_SEGS + 1], fcmax[MAX_SEGS], tile_off[MAX_SEGS + 1];
     int64_t fc_per_b, pool_per_b;
     int tt_per_b, K;
@@ -389,9 +397,9 @@ __global__ __launch_bounds__(CB) void cand_build_kernel(const BArgs ba) {
     const int m = min(max(cnt, 0), HEAD);
     ba.fcell[b * ba.fc_per_b + ba.fc_off[l] + c] = make_int2(cnt > 0 ? int(begin) : 0, cnt > 0 ? cnt4 | (m << 16) : cnt);
     if (cnt <= 0) return;
-    Cand *out = ba.pool + b * ba.pool_per_b + begin;
+    CandBlock *out = ba.pool + (b * ba.pool_per_b + begin) / 4;  // both multiples of 4
     // padding: points at infinity (their keys lose to every real point)
-    for (int i = cnt; i < cnt4; ++i) out[i] = Cand{INFINITY, INFINITY, -1};
+    for (int i = cnt; i < cnt4; ++i) put_cand(out, i, INFINITY, INFINITY, -1);
     float tb = top[0];
 #pragma unroll
     for (int i = 1; i < HEAD; ++i)
@@ -409,7 +417,7 @@ __global__ __launch_bounds__(CB) void cand_build_kernel(const BArgs ba) {
         }
         if (slot < m) used |= 1u << slot;
         else slot = tail++;
-        if (slot < cnt) out[slot] = Cand{pt.x, pt.y, __float_as_int(pt.z)};
+        if (slot < cnt) put_cand(out, slot, pt.x, pt.y, __float_as_int(pt.z));
     });
 }
 
@@ -421,7 +429,7 @@ struct CArgs {
     const void *ws;
     const FineParams *fp;
     const int2 *fcell;
-    const Cand *pool;
+    const CandBlock *pool;
     int fc_off[MAX_SEGS + 1];
     int64_t fc_per_b, pool_per_b;
     int pl_log2;  // lanes per row = 2^pl_log2 >= P
@@ -541,16 +549,15 @@ __global__ __launch_bounds__(THREADS) void deform_cand_kernel(const CArgs ka) {
             const int cy_raw = act && keff > 0 ? (inside[0] ? ce[0].y : -1) : 0;
             const int cnt = cy_raw > 0 ? cy_raw & 0xffff : cy_raw, head = cy_raw > 0 ? cy_raw >> 16 : 0;
             if (cnt > 0) {
-                // Lists are padded to whole 4-entry steps (points at infinity) and the
-                // next step's entries are loaded during this one (past a list's end
-                // they are other lists' entries, or the pool's slack, and unused).
-                // Within the sorted head a lane stops once the next entry's distance
-                // to the cell exceeds its K-th distance: the head is sorted by that
-                // distance, computed here exactly as the build computed it (same
-                // widened rectangle, no contraction), so it bounds the entry and
-                // every later one from below (scaled down a little against the
-                // rounding of either distance).  An unfilled K-th key reads as NaN,
-                // which never compares less.
+                // Lists are padded to whole 4-entry blocks (points at infinity); a
+                // lane reads one block per step.  Within the sorted head a lane stops
+                // once a block's last entry is farther from the cell than its K-th
+                // distance: the head is sorted by that distance, computed here exactly
+                // as the build computed it (same widened rectangle, no contraction),
+                // and the tail's entries are no nearer to the cell than the head's, so
+                // it bounds every later entry from below (scaled down a little against
+                // the rounding of either distance).  An unfilled K-th key reads as
+                // NaN, which never compares less.
                 FineParams f;
                 if (uni) f = ka.fp[b0 * L + l];
                 else f = ka.fp[b * L + l];
@@ -561,31 +568,22 @@ __global__ __launch_bounds__(THREADS) void deform_cand_kernel(const CArgs ka) {
                     const int cy = int(floorf(__fmul_rn(__fsub_rn(sy, f.y0), f.inv_s)));
                     rc = fine_rect(f, cy * f.gx + cx);
                 }
-                auto below = [&](const Cand &e) {
+                auto below = [&](const CandBlock &e) {  // the block's last entry
 #pragma clang fp contract(off)
-                    const float dx = fmaxf(0.f, fmaxf(rc.x0 - e.x, e.x - rc.x1));
-                    const float dy = fmaxf(0.f, fmaxf(rc.y0 - e.y, e.y - rc.y1));
+                    const float dx = fmaxf(0.f, fmaxf(rc.x0 - e.x[3], e.x[3] - rc.x1));
+                    const float dy = fmaxf(0.f, fmaxf(rc.y0 - e.y[3], e.y[3] - rc.y1));
                     return (dx * dx + dy * dy) * 0.999996f > key_d2(keys[KT - 1]);
                 };
-                const Cand *cp = ka.pool + b * ka.pool_per_b + ce[0].x;
+                const CandBlock *cp = ka.pool + (b * ka.pool_per_b + ce[0].x) / 4;  // both multiples of 4
                 const bool can_stop = keff == KT;
-                Cand ca[4], cb[4];
-#pragma unroll
-                for (int u = 0; u < 4; ++u) ca[u] = cp[u];
-                for (int i = 0;; i += 8) {
-                    if (can_stop && i < head && below(ca[0])) break;
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) cb[u] = cp[i + 4 + u];
+                CandBlock blk = cp[0];
+                for (int i = 0;; i += 4) {
 #pragma unroll
                     for (int u = 0; u < 4; ++u)
-                        topk_insert<KT>(keys, make_key(dist2(ca[u].x, ca[u].y, sx, sy), ca[u].row));
-                    if (i + 4 >= cnt || (can_stop && i + 4 < head && below(cb[0]))) break;
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) ca[u] = cp[i + 8 + u];
-#pragma unroll
-                    for (int u = 0; u < 4; ++u)
-                        topk_insert<KT>(keys, make_key(dist2(cb[u].x, cb[u].y, sx, sy), cb[u].row));
-                    if (i + 8 >= cnt) break;
+                        topk_insert<KT>(keys, make_key(dist2(blk.x[u], blk.y[u], sx, sy), blk.row[u]));
+                    // entry i + 3 in the head bounds every later entry
+                    if (i + 4 >= cnt || (can_stop && i + 4 <= head && below(blk))) break;
+                    blk = cp[i / 4 + 1];
                 }
             } else if (cnt < 0) {
                 const SegView g = seg_view(ka.ws, ka.wl, ka.segs, b, l);
@@ -899,7 +897,7 @@ aff_status launch_deform_k(const aff_deform_args &a, const Segs &segs, const DLa
     ba.fp = reinterpret_cast<FineParams *>(w + dl.fparams);
     ba.fcell = reinterpret_cast<int2 *>(w + dl.fcell);
     ba.counter = reinterpret_cast<int *>(w + dl.counter);
-    ba.pool = reinterpret_cast<Cand *>(w + dl.pool);
+    ba.pool = reinterpret_cast<CandBlock *>(w + dl.pool);
     for (int l = 0; l <= segs.L; ++l) {
         ba.fc_off[l] = dl.fc_off[l];
         ba.tile_off[l] = dl.tile_off[l];
