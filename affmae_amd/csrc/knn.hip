@@ -424,6 +424,39 @@ __device__ __forceinline__ bool visit_disk_win(const GridParams &p, const Window
     return covered;
 }
 
+// The starting radius^2 of a lane's window search: u scaled so that the
+// expected number of points in the disk is `target`.  The expectation sums,
+// over the grid rows whose centre line meets the disk, the points of the cells
+// the chord along that line spans, end cells in proportion to their covered
+// width (cell counts from the window's cell table).  Returns u unchanged when
+// the disk reaches outside the window.  Only the number of refinement passes
+// depends on it: every pass still counts exactly.
+__device__ __forceinline__ float window_radius2(const GridParams &p, const Window &w, float qx, float qy, float u,
+                                               float target) {
+    const float rad = __builtin_amdgcn_sqrtf(u);
+    const int cy0 = cell_coord(qy - rad, p.y0, p.inv_h, p.gy), cy1 = cell_coord(qy + rad, p.y0, p.inv_h, p.gy);
+    if (cy0 < w.wy0 || cy1 > w.wy1) return u;
+    float est = 0.f;
+    bool inside = true;
+    for (int cy = cy0; cy <= cy1; ++cy) {
+        const float dy = p.y0 + (float(cy) + 0.5f) * p.h - qy;
+        const float w2 = u - dy * dy;
+        if (!(w2 > 0.f)) continue;
+        const float hw = __builtin_amdgcn_sqrtf(w2);
+        const float xa = qx - hw, xb = qx + hw;
+        const int ca = cell_coord(xa, p.x0, p.inv_h, p.gx), cb = cell_coord(xb, p.x0, p.inv_h, p.gx);
+        inside = inside && ca >= w.wx0 && cb <= w.wx1;
+        const int *row = w.wcs + (cy - w.wy0) * w.wx1p - w.wx0;
+        const int ia = min(max(ca, w.wx0), w.wx1), ib = min(max(cb, w.wx0), w.wx1);
+        const float na = float(row[ia + 1] - row[ia]), nb = float(row[ib + 1] - row[ib]);
+        // uncovered fractions of the end cells
+        const float fa = fminf(fmaxf((xa - (p.x0 + float(ia) * p.h)) * p.inv_h, 0.f), 1.f);
+        const float fb = fminf(fmaxf((p.x0 + float(ib + 1) * p.h - xb) * p.inv_h, 0.f), 1.f);
+        est += float(row[ib + 1] - row[ia]) - fa * na - fb * nb;
+    }
+    return inside ? u * target / fmaxf(est, 1.f) : u;
+}
+
 // visit_disk() reporting the point's slot in the cell-ordered array too:
 // f(d2, slot, index).
 template <typename F>
@@ -618,8 +651,11 @@ __global__ __launch_bounds__(WIN_THREADS) void knn_win_kernel(const float4 *__re
     bool from_win = false;
     if (active && win) {
         const Window w{s_xy, s_wcs, wx0, wy0, wx1, wy1, WX + 1};
+        // (more waves than fit at once: total work counts, and the refined start saves
+        // a wave most of a radius pass; in one resident generation it only adds latency)
+        const float Uw = ROWS ? window_radius2(p, w, qx, qy, U0, 0.5f * float(k + CAP)) : U0;
         cnt = radius_select<CAP>(
-            [&](float U, auto &&f) { return visit_disk_win(p, w, qx, qy, U, slack, f); }, U0, k, s_list, lane, hi);
+            [&](float U, auto &&f) { return visit_disk_win(p, w, qx, qy, U, slack, f); }, Uw, k, s_list, lane, hi);
         from_win = cnt >= 0;
     }
     if (active && cnt < 0) {
@@ -778,9 +814,10 @@ extern "C" aff_status aff_knn(const float *query, int64_t q_sb, int64_t q_sm, co
                         : (rows ? knn::knn_win_kernel<64, knn::WMAX, knn::WCMAX, true>
                                 : knn::knn_win_kernel<64, knn::WMAX, knn::WCMAX, false>);
         };
-        // More waves than fit at once: the launch is throughput bound, and whole-row
-        // stores (through LDS) cost the memory path far less than one word per row per
-        // store.  One resident generation: the direct stores end each wave sooner.
+        // More waves than fit at once: the launch is throughput bound; whole-row stores
+        // (through LDS) cost the memory path far less than one word per row per store,
+        // and the starting radius is refined from the window's cell counts.  One
+        // resident generation: the direct stores and unrefined start end each wave sooner.
         const WinFn direct = pick(false);
         const int64_t waves = (int64_t)gridd.x * gridd.y;
         const bool rows =
