@@ -226,8 +226,18 @@ __device__ __forceinline__ float initial_radius2(const SegView &g, float qx, flo
     const int cx = cell_coord(qx, p.x0, p.inv_h, p.gx), cy = cell_coord(qy, p.y0, p.inv_h, p.gy);
     const int ax0 = max(cx - 2, 0), ax1 = min(cx + 2, p.gx - 1);
     const int ay0 = max(cy - 2, 0), ay1 = min(cy + 2, p.gy - 1);
+    // the (at most 5) rows' offsets loaded together, then summed
+    int lo[5], hi[5];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+        const int y = min(ay0 + i, ay1);
+        lo[i] = g.cs[y * p.gx + ax0];
+        hi[i] = g.cs[y * p.gx + ax1 + 1];
+    }
     int cntw = 0;
-    for (int y = ay0; y <= ay1; ++y) cntw += g.cs[y * p.gx + ax1 + 1] - g.cs[y * p.gx + ax0];
+#pragma unroll
+    for (int i = 0; i < 5; ++i)
+        if (ay0 + i <= ay1) cntw += hi[i] - lo[i];
     const float h2 = p.h * p.h;
     const float rho = cntw > 0 ? float(cntw) / (float((ax1 - ax0 + 1) * (ay1 - ay0 + 1)) * h2)
                                : float(g.n) / (float(p.ncell) * h2);

@@ -631,15 +631,42 @@ __global__ __launch_bounds__(WIN_THREADS) void knn_win_kernel(const float4 *__re
             }
             if (lane == 0) s_rb[WY] = total;
             __syncthreads();
-            for (int e = lane; e < (WX + 1) * WY; e += WIN_THREADS) {
+            // cell table and points: each lane's loads are issued together, then
+            // written, so the copy costs one memory round trip, not one per entry
+            constexpr int WCI = (WC + WIN_THREADS - 1) / WIN_THREADS;
+            const int ne = (WX + 1) * WY;
+            int cv[WCI];
+#pragma unroll
+            for (int u = 0; u < WCI; ++u) {
+                const int e = min(lane + u * WIN_THREADS, ne - 1);
                 const int r = e / (WX + 1), c = e - r * (WX + 1);
-                s_wcs[e] = s_rb[r] + g.cs[(wy0 + r) * p.gx + wx0 + c] - s_gb[r];
+                cv[u] = g.cs[(wy0 + r) * p.gx + wx0 + c];
             }
-            for (int t = lane; t < total; t += WIN_THREADS) {
-                const int r = s_rowof[t];
-                const float4 pt = g.P[s_gb[r] + (t - s_rb[r])];
-                s_xy[t] = make_float2(pt.x, pt.y);
-                s_id[t] = uint16_t(__float_as_int(pt.z));
+#pragma unroll
+            for (int u = 0; u < WCI; ++u) {
+                const int e = lane + u * WIN_THREADS;
+                if (e < ne) {
+                    const int r = e / (WX + 1);
+                    s_wcs[e] = s_rb[r] + cv[u] - s_gb[r];
+                }
+            }
+            constexpr int PB = 8;  // points per lane in flight
+            for (int t0 = 0; t0 < total; t0 += PB * WIN_THREADS) {
+                float4 pt[PB];
+#pragma unroll
+                for (int u = 0; u < PB; ++u) {
+                    const int t = min(t0 + u * WIN_THREADS + lane, total - 1);
+                    const int r = s_rowof[t];
+                    pt[u] = g.P[s_gb[r] + (t - s_rb[r])];
+                }
+#pragma unroll
+                for (int u = 0; u < PB; ++u) {
+                    const int t = t0 + u * WIN_THREADS + lane;
+                    if (t < total) {
+                        s_xy[t] = make_float2(pt[u].x, pt[u].y);
+                        s_id[t] = uint16_t(__float_as_int(pt[u].z));
+                    }
+                }
             }
             __syncthreads();
         }
