@@ -36,6 +36,37 @@ def _power_ptr(power, dev):
     return p
 
 
+def get_fused_knn_config(B: int, N: int, H: int, K: int, C_: int, L: int = 1, knn_k: int = 4) -> dict:
+    """Launch shape of the fused KNN + deformable kernel for these sizes.
+
+    Counterpart of ``get_fused_knn_config`` (fused_deform_attn.py:744-790), which
+    picks Triton block sizes from a benchmark table.  The HIP kernel has no tuned
+    parameters: its shape follows from the sizes exactly as ``aff_deform_fwd``
+    derives it (K = sampling points per head and level, knn_k = neighbours per
+    sample).  One wave takes ``rows_per_wave`` consecutive (batch, query, head)
+    rows, one lane per (row, point) during the search; each row's gather uses
+    C_ / 8 lanes of 8 channels with ``gather_rows_in_flight`` value rows in flight.
+    """
+    if min(B, N, H, K, C_, L, knn_k) < 1:
+        raise ValueError("get_fused_knn_config: sizes must be >= 1")
+    pl = max(0, (K - 1).bit_length())
+    rows_per_wave = 64 >> pl
+    pair_group = 8
+    skp = (L * K * knn_k + pair_group - 1) // pair_group * pair_group
+    per_wave = 8 * rows_per_wave * skp
+    waves = 4 if per_wave * 4 <= 65536 else 1
+    rows = B * N * H
+    return {
+        "rows_per_wave": rows_per_wave,
+        "lanes_per_row_search": 1 << pl,
+        "lanes_per_row_gather": max(1, C_ // 8),
+        "waves_per_workgroup": waves,
+        "workgroups": -(-rows // (rows_per_wave * waves)),
+        "lds_bytes_per_workgroup": per_wave * waves,
+        "gather_rows_in_flight": pair_group,
+    }
+
+
 def deform_launch(query_pos, kv_pos, level_start, offsets, attn, values, power, K, mode, return_knn=False):
     """aff_deform_fwd.
 

@@ -159,3 +159,19 @@ def test_pre_table_matches_oracle(oracle_mod):
     from affmae_amd.utils.pos_embed import pre_table_fp32
     import numpy as np
     np.testing.assert_allclose(pre_table_fp32.numpy(), oracle_mod.pre_table(), rtol=1e-6, atol=1e-6)
+
+
+def test_fused_knn_config_matches_launch():
+    """The reported launch shape follows aff_deform_fwd: cfg4 (4 levels x 4 points,
+    3 neighbours, C=32) takes 16 rows per wave and 24 576 bytes of LDS per 4-wave
+    workgroup, the figure the kernel trace records for deform_cand_kernel."""
+    from affmae_amd.kernels.fused_deform_attn import get_fused_knn_config
+    c = get_fused_knn_config(32, 12544, 8, 4, 32, L=4, knn_k=3)
+    assert c["rows_per_wave"] == 16 and c["lanes_per_row_search"] == 4
+    assert c["waves_per_workgroup"] == 4 and c["lds_bytes_per_workgroup"] == 24576
+    assert c["workgroups"] == 32 * 12544 * 8 // 64
+    assert c["lanes_per_row_gather"] == 4 and c["gather_rows_in_flight"] == 8
+    one = get_fused_knn_config(2, 1000, 6, 1, 64)
+    assert one["rows_per_wave"] == 64 and one["lanes_per_row_search"] == 1
+    with pytest.raises(ValueError):
+        get_fused_knn_config(0, 1, 1, 1, 1)
