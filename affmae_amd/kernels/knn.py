@@ -96,6 +96,19 @@ def knn_hip(query, ref, k, D=2):
     return KNNFunction.apply(query, ref, k, D)
 
 
+def knn_pytorch_large(query, ref, k):
+    """int64 [B,M,k] (knn.py:1312-1332).  The reference materialises cdist + topk;
+    here the exact HIP KNN serves it (ties: lower index first, where topk leaves
+    the order unspecified)."""
+    return knn_hip(query, ref, k, D=query.shape[-1])
+
+
+def knn_large_k_fallback(query, ref, k):
+    """int64 [B,M,k] (knn.py:1335-1365): the reference's k > 8 dispatch to KeOps or
+    cdist; the exact HIP KNN covers every k here."""
+    return knn_hip(query, ref, k, D=query.shape[-1])
+
+
 def knn(query, database, k, return_dist=False, D=None):
     """Public KNN (knn.py:1615-1648): int64 indices and optional squared distances.
 

@@ -84,6 +84,13 @@ class ClusterAttention(nn.Module):
             self._pe_table_cache[key] = tab
         return tab
 
+    def _make_pos_bias(self, pe_idx: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+        """The dense bias [B,H,N,M] of pe_idx (attention.py:72-125), for callers that want
+        it materialised.  forward() never builds it: the attention kernel reads the
+        table row of each (query, neighbour) pair itself.  bf16 is accepted."""
+        tab = self.pe_table(dtype)                                   # [T*T, H]
+        return tab[pe_idx.long()].permute(0, 3, 1, 2).to(dtype)
+
     def forward(self, feat, member_idx, cluster_mask, pe_idx, global_attn: bool):
         """feat [B,N,C], member_idx / pe_idx [B,N,M], cluster_mask [B,N,M] or None -> [B,N,C]."""
         B, N, C = feat.shape

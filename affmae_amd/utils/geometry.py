@@ -16,6 +16,19 @@ from ..kernels.knn import knn as hip_knn
 from ..kernels.weighted_gather import weighted_gather
 
 
+def knn_keops(query, database, k, return_dist=False):
+    """geometry.py:56-95: int64 indices [b,n_,k] of the k nearest database points and,
+    with return_dist, their Euclidean distances (the reference's KeOps Kmin of
+    sqrt(sum (q - x)^2)), from the exact HIP KNN in fp32, no autograd."""
+    with torch.no_grad():
+        q = query.detach().float()
+        d = database.detach().float()
+        if not return_dist:
+            return hip_knn(q, d, k)
+        idx, d2 = hip_knn(q, d, k, return_dist=True)
+        return idx, d2.sqrt()
+
+
 def inverse_distance_weighting(dist, power=3):
     """w = (1 / (d^p + 1e-10)) / (sum + 1e-12) in fp32 (callers pass squared distances)."""
     with torch.autocast(device_type=dist.device.type, enabled=False):

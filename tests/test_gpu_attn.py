@@ -246,3 +246,44 @@ def test_autograd_function_forward(oracle_mod, dev):
     out = FlashLocalAttentionFunction.apply(g["q"], g["k"], g["v"], g["idx"], g["bias"], None, g["bk"], g["bv"], 0.3)
     ro, _ = _oracle(oracle_mod, c, 0.3)
     _assert_fp32(out, None, ro, None)
+
+
+# ----------------------------------------------------- ClusterAttention module --
+@pytest.mark.parametrize("with_mask", [False, True])
+def test_cluster_attention_module(oracle_mod, dev, with_mask):
+    """ClusterAttention.forward (attention.py:127-207) against the oracle: the module's own
+    q / kv / proj weights, per-head interleaved [k_h | v_h], the table bias built
+    from the oracle's pre_table and pe_index, the cluster mask and the blank token.
+    Also pins _make_pos_bias to the oracle's dense table bias."""
+    from affmae_amd.layers import ClusterAttention
+    B, N, C, H, M = 2, 512, 64, 2, 48
+    Ch = C // H
+    pos = torch.floor(workloads.cfg1_coords(B, N, seed=3) * 32)
+    pos_d = pos.to(dev)
+    idx = knn(pos_d, pos_d, M)
+    idx_np = idx.cpu().numpy()
+    pe = oracle_mod.pe_index(pos.numpy(), idx_np)
+    torch.manual_seed(5)
+    m = ClusterAttention(C, H).to(dev).eval()
+    with torch.no_grad():
+        m.blank_k.normal_(0, 0.3)
+        m.blank_v.normal_(0, 0.3)
+    g = torch.Generator().manual_seed(6)
+    feat = torch.randn((B, N, C), generator=g)
+    cmask = (torch.rand((B, N, M), generator=g) > 0.2) if with_mask else None
+    with torch.no_grad():
+        out = m(feat.to(dev), idx, None if cmask is None else cmask.to(dev), torch.from_numpy(pe).to(dev), False)
+        w, bb = m.pos_embed.weight.double().cpu().numpy(), m.pos_embed.bias.double().cpu().numpy()
+        table = (oracle_mod.pre_table().astype(np.float64) @ w.T + bb).astype(np.float32)
+        dense = oracle_mod.table_bias(pe, table).astype(np.float32)
+        pb = m._make_pos_bias(torch.from_numpy(pe).to(dev), torch.float32)
+        np.testing.assert_allclose(_np(pb), dense, rtol=1e-6, atol=1e-6)
+        q = m.q(feat.to(dev)).view(B, N, H, Ch).permute(0, 2, 1, 3)
+        kv = m.kv(feat.to(dev)).view(B, N, H, 2 * Ch).permute(0, 2, 1, 3)
+        ro, _ = oracle_mod.nbhd_attn(_np(q), _np(kv[..., :Ch]), _np(kv[..., Ch:]), idx_np, m.scale, bias=dense,
+                                     mask=None if cmask is None else cmask.unsqueeze(1).numpy(),
+                                     blank_k=_np(m.blank_k.view(H, Ch)), blank_v=_np(m.blank_v.view(H, Ch)))
+        ref = m.proj(torch.from_numpy(ro.astype(np.float32)).to(dev).permute(0, 2, 1, 3).reshape(B, N, C))
+    scale = float(ref.abs().max())
+    err = float((out - ref).abs().max())
+    assert err <= 1e-5 * max(scale, 1.0), f"rel err {err / scale:.3e}"

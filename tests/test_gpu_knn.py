@@ -144,3 +144,22 @@ def test_k_too_large_raises(dev):
     pos = torch.rand(1, 10, 2, device=dev)
     with pytest.raises(AssertionError, match="exceeds number of reference points"):
         knn(pos, pos, 11)
+
+
+def test_reference_fallback_names(oracle_mod, dev):
+    """knn_large_k_fallback / knn_pytorch_large (knn.py:1312-1365) and knn_keops
+    (geometry.py:56-95, Euclidean distances) give the exact neighbours."""
+    from affmae_amd.kernels.knn import knn_large_k_fallback, knn_pytorch_large
+    from affmae_amd.utils.geometry import knn_keops
+    pos = workloads.cfg1_coords(B=2, N=700, seed=21)
+    q = pos[:, :300]
+    oi, od = oracle_mod.knn(q.numpy(), pos.numpy(), 20)
+    for fn in (knn_large_k_fallback, knn_pytorch_large):
+        idx = fn(q.to(dev), pos.to(dev), 20)
+        assert idx.dtype == torch.int64
+        np.testing.assert_array_equal(idx.cpu().numpy(), oi)
+    idx, dist = knn_keops(q.to(dev).half(), pos.to(dev).half(), 20, return_dist=True)
+    oih, odh = oracle_mod.knn(q.half().float().numpy(), pos.half().float().numpy(), 20)
+    np.testing.assert_array_equal(idx.cpu().numpy(), oih)
+    np.testing.assert_allclose(dist.cpu().numpy(), np.sqrt(odh.astype(np.float64)), rtol=1e-6)
+    np.testing.assert_array_equal(knn_keops(q.to(dev), pos.to(dev), 20).cpu().numpy(), oi)
