@@ -253,3 +253,32 @@ def test_deformable_modules_branches_agree(dev):
     with torch.no_grad():
         y = s(q, qp)
     assert y.shape == q.shape and torch.isfinite(y).all()
+
+
+@pytest.mark.parametrize("self_attn", [False, True])
+def test_deformable_module_against_oracle(oracle_mod, dev, self_attn):
+    """DeformableCross/SelfAttention.forward (attention.py:275-404, 472-593) against the
+    oracle: the module's own sampling_offsets / attention_weights (softmax over the 4
+    points) / value_proj viewed [b, n_kv, h, c_] / output_proj, learnable Shepard power."""
+    torch.manual_seed(4)
+    d, h, p = 64, 4, 4
+    m = (DeformableSelfAttention if self_attn else DeformableCrossAttention)(d, h, p).to(dev).eval()
+    with torch.no_grad():
+        m.sampling_offsets.weight.normal_(0, 0.02)
+        m.attention_weights.weight.normal_(0, 0.2)
+        m.shepard_power.fill_(1.3)
+    g = torch.Generator().manual_seed(8)
+    q = torch.randn((2, 300, d), generator=g).to(dev)
+    qp = torch.rand((2, 300, 2), generator=g).to(dev)
+    kv = q if self_attn else torch.randn((2, 450, d), generator=g).to(dev)
+    kp = qp if self_attn else torch.rand((2, 450, 2), generator=g).to(dev)
+    with torch.no_grad():
+        out = m(q, qp) if self_attn else m(q, qp, kv, kp)
+        b, n_q, n_kv = 2, 300, kv.shape[1]
+        off = m.sampling_offsets(q).view(b, n_q, h, 1, p, 2)
+        att = torch.softmax(m.attention_weights(q).view(b, n_q, h, p), -1).view(b, n_q, h, 1, p)
+        val = m.value_proj(kv).view(b, n_kv, h, d // h)
+        ro, _ = oracle_mod.deform(_np(qp), _np(kp), [0, n_kv], _np(off), _np(att), _np(val), 1.3, 4, "shepard")
+        ref = m.output_proj(torch.from_numpy(ro.astype(np.float32)).to(dev).reshape(b, n_q, d))
+    scale = float(ref.abs().max())
+    assert float((out - ref).abs().max()) <= 1e-5 * max(scale, 1.0)
