@@ -183,9 +183,12 @@ __global__ __launch_bounds__(BUILD_THREADS) void grid_build_kernel(const float *
     auto cell_of = [&](float x, float y) {
         return cell_coord(y, p.y0, p.inv_h, p.gy) * p.gx + cell_coord(x, p.x0, p.inv_h, p.gx);
     };
+    int cl[PPT];  // each point's cell, for both passes
 #pragma unroll
-    for (int j = 0; j < PPT; ++j)
-        if (tid + j * BUILD_THREADS < n) atomicAdd(&s_cnt[cell_of(rx[j], ry[j])], 1);
+    for (int j = 0; j < PPT; ++j) {
+        cl[j] = cell_of(rx[j], ry[j]);
+        if (tid + j * BUILD_THREADS < n) atomicAdd(&s_cnt[cl[j]], 1);
+    }
     for (int i = tid + PPT * BUILD_THREADS; i < n; i += BUILD_THREADS)
         atomicAdd(&s_cnt[cell_of(R[(int64_t)i * sn], R[(int64_t)i * sn + 1])], 1);
     __syncthreads();
@@ -198,7 +201,7 @@ __global__ __launch_bounds__(BUILD_THREADS) void grid_build_kernel(const float *
     for (int j = 0; j < PPT; ++j) {
         const int i = tid + j * BUILD_THREADS;
         if (i < n) {
-            const int slot = atomicAdd(&s_cnt[cell_of(rx[j], ry[j])], 1);
+            const int slot = atomicAdd(&s_cnt[cl[j]], 1);
             pts[slot] = make_float4(rx[j], ry[j], __int_as_float(s.start[l] + i), 0.f);
         }
     }
@@ -231,15 +234,27 @@ __global__ __launch_bounds__(BUILD_THREADS) void grid_build_kernel(const float *
     const int T = max(1, (int)rintf(sqrtf(float(TILE_QUERIES) * float(ncell) / float(max(M, 1)))));
     const int ntx = (p.gx + T - 1) / T, nty = (p.gy + T - 1) / T;
     const int ntile = ntx * nty;
+    // c / T for 0 <= c < 2^24 without an integer division: a float quotient,
+    // corrected by one either way
+    const float inv_t = 1.f / float(T);
+    auto div_t = [&](int c) {
+        int d = int(float(c) * inv_t);
+        d -= d * T > c ? 1 : 0;
+        d += (d + 1) * T <= c ? 1 : 0;
+        return d;
+    };
     auto tile_of = [&](float x, float y) {
-        const int tx = cell_coord(x, p.x0, p.inv_h, p.gx) / T, ty = cell_coord(y, p.y0, p.inv_h, p.gy) / T;
+        const int tx = div_t(cell_coord(x, p.x0, p.inv_h, p.gx)), ty = div_t(cell_coord(y, p.y0, p.inv_h, p.gy));
         return ty * ntx + ((ty & 1) ? ntx - 1 - tx : tx);
     };
     for (int c = tid; c < ntile; c += BUILD_THREADS) s_cnt[c] = 0;
     __syncthreads();
+    int tl[PPT];  // each query's tile, for both passes
 #pragma unroll
-    for (int j = 0; j < PPT; ++j)
-        if (tid + j * BUILD_THREADS < M) atomicAdd(&s_cnt[tile_of(qx[j], qy[j])], 1);
+    for (int j = 0; j < PPT; ++j) {
+        tl[j] = tile_of(qx[j], qy[j]);
+        if (tid + j * BUILD_THREADS < M) atomicAdd(&s_cnt[tl[j]], 1);
+    }
     for (int i = tid + PPT * BUILD_THREADS; i < M; i += BUILD_THREADS)
         atomicAdd(&s_cnt[tile_of(Q[(int64_t)i * qb.q_sm], Q[(int64_t)i * qb.q_sm + 1])], 1);
     __syncthreads();
@@ -248,7 +263,7 @@ __global__ __launch_bounds__(BUILD_THREADS) void grid_build_kernel(const float *
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
         const int i = tid + j * BUILD_THREADS;
-        if (i < M) qo[atomicAdd(&s_cnt[tile_of(qx[j], qy[j])], 1)] = make_float4(qx[j], qy[j], __int_as_float(i), 0.f);
+        if (i < M) qo[atomicAdd(&s_cnt[tl[j]], 1)] = make_float4(qx[j], qy[j], __int_as_float(i), 0.f);
     }
     for (int i = tid + PPT * BUILD_THREADS; i < M; i += BUILD_THREADS) {
         const float x = Q[(int64_t)i * qb.q_sm], y = Q[(int64_t)i * qb.q_sm + 1];
