@@ -62,16 +62,16 @@ struct FineParams {
 // list starts with its HEAD points nearest to the cell sorted by that distance
 // (the head), so within the head the distance of an entry to the cell bounds
 // the distances of every later entry from below.
-// Entries are stored four to a block, fields apart, so that a scan step reads
-// a block as three 16-byte loads (lists start and end on block boundaries).
+// Entries are stored four to a block, the rows apart from the points, so that a
+// scan step reads a block as three 16-byte loads and the build writes an entry
+// with two stores (lists start and end on block boundaries).
 struct alignas(16) CandBlock {
-    float x[4], y[4];
+    float2 xy[4];
     int row[4];
 };
 __device__ __forceinline__ void put_cand(CandBlock *blk, int slot, float x, float y, int row) {
     CandBlock &c = blk[slot >> 2];
-    c.x[slot & 3] = x;
-    c.y[slot & 3] = y;
+    c.xy[slot & 3] = make_float2(x, y);
     c.row[slot & 3] = row;
 }
 
@@ -570,8 +570,8 @@ __global__ __launch_bounds__(THREADS) void deform_cand_kernel(const CArgs ka) {
                 }
                 auto below = [&](const CandBlock &e) {  // the block's last entry
 #pragma clang fp contract(off)
-                    const float dx = fmaxf(0.f, fmaxf(rc.x0 - e.x[3], e.x[3] - rc.x1));
-                    const float dy = fmaxf(0.f, fmaxf(rc.y0 - e.y[3], e.y[3] - rc.y1));
+                    const float dx = fmaxf(0.f, fmaxf(rc.x0 - e.xy[3].x, e.xy[3].x - rc.x1));
+                    const float dy = fmaxf(0.f, fmaxf(rc.y0 - e.xy[3].y, e.xy[3].y - rc.y1));
                     return (dx * dx + dy * dy) * 0.999996f > key_d2(keys[KT - 1]);
                 };
                 const CandBlock *cp = ka.pool + (b * ka.pool_per_b + ce[0].x) / 4;  // both multiples of 4
@@ -580,7 +580,7 @@ __global__ __launch_bounds__(THREADS) void deform_cand_kernel(const CArgs ka) {
                 for (int i = 0;; i += 4) {
 #pragma unroll
                     for (int u = 0; u < 4; ++u)
-                        topk_insert<KT>(keys, make_key(dist2(blk.x[u], blk.y[u], sx, sy), blk.row[u]));
+                        topk_insert<KT>(keys, make_key(dist2(blk.xy[u].x, blk.xy[u].y, sx, sy), blk.row[u]));
                     // entry i + 3 in the head bounds every later entry
                     if (i + 4 >= cnt || (can_stop && i + 4 <= head && below(blk))) break;
                     blk = cp[i / 4 + 1];
