@@ -350,7 +350,7 @@ __device__ __forceinline__ void tile_of(const BArgs &ba, int &b, int &l, int &t,
 // with points at infinity; its cell entry holds (begin, padded length | head
 // length << 16).  Lists longer than MAX_CAND, or beyond the pool, get count
 // -1: their samples search the coarse grid.
-constexpr int HEAD = 16;
+constexpr int HEAD = 12;  // sorted head length: 16 and 8 both timed slower at cfg4
 
 template <int KT>
 __global__ __launch_bounds__(CB) void cand_build_kernel(const BArgs ba) {
