@@ -99,6 +99,7 @@ struct QueryBin {
     int64_t q_sb, q_sm;
     int M;
     float4 *out;
+    int tile_queries;  // queries per tile; TILE_QUERIES when 0
 };
 
 // Optional: ints the build sets to zero before anything that runs after it on

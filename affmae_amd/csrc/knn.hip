@@ -213,7 +213,7 @@ __global__ __launch_bounds__(BUILD_THREADS) void grid_build_kernel(const float *
     if (qb.out == nullptr) return;
 
     // 6. queries by tile of this grid: square T x T cell tiles holding about
-    // TILE_QUERIES queries each, visited in serpentine order (tile rows
+    // qb.tile_queries queries each, visited in serpentine order (tile rows
     // alternate direction), so consecutive tiles always touch
     __syncthreads();
     const int M = qb.M;
@@ -231,7 +231,8 @@ __global__ __launch_bounds__(BUILD_THREADS) void grid_build_kernel(const float *
             qy[j] = Q[(int64_t)i * qb.q_sm + 1];
         }
     }
-    const int T = max(1, (int)rintf(sqrtf(float(TILE_QUERIES) * float(ncell) / float(max(M, 1)))));
+    const int tq = qb.tile_queries > 0 ? qb.tile_queries : TILE_QUERIES;
+    const int T = max(1, (int)rintf(sqrtf(float(tq) * float(ncell) / float(max(M, 1)))));
     const int ntx = (p.gx + T - 1) / T, nty = (p.gy + T - 1) / T;
     const int ntile = ntx * nty;
     // c / T for 0 <= c < 2^24 without an integer division: a float quotient,
@@ -286,12 +287,12 @@ aff_status launch_build(const float *src, int64_t sb, int64_t sn, int B, const S
 
 aff_status launch_build(const float *src, int64_t sb, int64_t sn, int B, const Segs &s, void *ws,
                         hipStream_t stream, const ZeroSpan &z) {
-    return launch_build_impl(src, sb, sn, B, s, ws, stream, QueryBin{nullptr, 0, 0, 0, nullptr}, z);
+    return launch_build_impl(src, sb, sn, B, s, ws, stream, QueryBin{nullptr, 0, 0, 0, nullptr, 0}, z);
 }
 
 aff_status launch_build(const float *src, int64_t sb, int64_t sn, int B, const Segs &s, void *ws,
                         hipStream_t stream) {
-    return launch_build(src, sb, sn, B, s, ws, stream, QueryBin{nullptr, 0, 0, 0, nullptr});
+    return launch_build(src, sb, sn, B, s, ws, stream, QueryBin{nullptr, 0, 0, 0, nullptr, 0});
 }
 
 }  // namespace grid
@@ -830,14 +831,16 @@ extern "C" aff_status aff_knn(const float *query, int64_t q_sb, int64_t q_sm, co
     hipStream_t st = static_cast<hipStream_t>(stream);
     const bool windowed = k <= 64 && N <= knn::MAX_SLOT;
     float4 *qsorted = reinterpret_cast<float4 *>(static_cast<char *>(ws) + L.total);
-    const grid::QueryBin qb{query, q_sb, q_sm, M, windowed ? qsorted : nullptr};
+    // sparser queries (M < N / 2) take the wide window and smaller tiles (32 queries,
+    // measured faster at cfg3); as dense as the points, 48 (32 was slower at cfg2)
+    const bool wide = 2 * (int64_t)M < (int64_t)N;
+    const grid::QueryBin qb{query, q_sb, q_sm, M, windowed ? qsorted : nullptr, wide ? 32 : 48};
     aff_status r = grid::launch_build(ref, r_sb, r_sn, B, s, ws, st, qb);
     if (r != AFF_OK) return r;
     dim3 block(knn::QUERY_THREADS);
     dim3 gridd((M + knn::QUERY_THREADS - 1) / knn::QUERY_THREADS, B);
     if (windowed) {
         // sparser queries spread a wave's 64 queries over more points: take the wider window
-        const bool wide = 2 * (int64_t)M < (int64_t)N;
         using WinFn = void (*)(const float4 *, const grid::Segs, const void *, grid::WsLayout, int, int, void *, int,
                                float *);
         auto pick = [&](bool rows) -> WinFn {
