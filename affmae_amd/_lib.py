@@ -84,6 +84,7 @@ SIGNATURES = {
     "aff_knn": (I32, [P, I64, I64, P, I64, I64, I32, I32, I32, I32, I32, P, I32, P, P, SZ, P]),
     "aff_nbhd_attn_workspace_bytes": (SZ, [ctypes.POINTER(NbhdAttnArgs)]),
     "aff_nbhd_attn_fwd": (I32, [ctypes.POINTER(NbhdAttnArgs), P]),
+    "aff_nbhd_attn_path": (I32, [ctypes.POINTER(NbhdAttnArgs)]),
     "aff_weighted_features_fwd": (I32, [P, I32, I64, I64, I64, I64, P, I32, I64, I64, P, I32, I64, I64,
                                         I32, I32, I32, I32, I32, I32, P, I64, I64, I64, P]),
     "aff_weighted_gather_fwd": (I32, [P, I32, I64, I64, P, I32, I64, I64, P, I32, I64, I64,

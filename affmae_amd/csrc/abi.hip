@@ -3,6 +3,8 @@
 
 #include <string.h>
 
+#include <mutex>
+
 namespace aff {
 
 static thread_local char g_last_error[512] = "";
@@ -17,16 +19,19 @@ aff_status fail(aff_status code, const char *fmt, ...) {
 
 void clear_error() { g_last_error[0] = '\0'; }
 
+// CU count of the current device, queried once per device (std::call_once, so
+// concurrent first calls from several host threads are ordered).
 int device_cu_count() {
     constexpr int MAXDEV = 64;
-    static int cache[MAXDEV];  // 0 = not queried yet; benign race: every writer stores the same value
+    static std::once_flag once[MAXDEV];
+    static int cache[MAXDEV];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAXDEV) return 256;
-    if (cache[dev] == 0) {
+    std::call_once(once[dev], [dev] {
         int n = 0;
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
         cache[dev] = n;
-    }
+    });
     return cache[dev];
 }
 

@@ -6,9 +6,12 @@
 // blank token joins the softmax after the neighbours, the running maximum
 // starts at -1e11 and LSE = m + log(l + 1e-12).
 //
-// Two kernels implement it.
+// Three kernels implement it; the host picks the first that takes the call.
 //
-// nbhd_attn_tile_kernel (bf16 / fp16, head_dim 32, M <= 64): one workgroup
+// nbhd_attn_wave_kernel (bf16 / fp16, head_dim 32, M <= 64, H * M <= 192):
+// one wave per head over a 32-query tile, described where it is defined.
+//
+// nbhd_attn_tile_kernel (bf16 / fp16, head_dim 32, M <= 64, any H): one workgroup
 // takes 32 consecutive queries of one image and every head.  The tile's
 // neighbour indices are deduplicated into a "union" of at most 224 token
 // rows (an LDS bitmap over the tile's index window plus a popcount prefix
@@ -31,7 +34,7 @@
 // by nbhd_attn_tile_fallback_kernel, launched right after on the same stream,
 // with the per-row routine below.
 //
-// nbhd_attn_fwd_kernel (every dtype and head_dim): D/8 lanes own one
+// nbhd_attn_fwd_kernel (every dtype and head_dim, the rest): D/8 lanes own one
 // (b, h, n) row (8 channels each).  Neighbours are consumed 8 at a time:
 // indices, mask, bias and 16 K/V row pieces are loaded before use, then one
 // online-softmax rescale is applied per block.
@@ -646,7 +649,10 @@ __global__ __launch_bounds__(THREADS) void nbhd_attn_tile_kernel(const aff_nbhd_
         // P row q overwrites S row q: clear the row's P span first (every union
         // slot a query does not use must read 0).  The 8 lanes of a query are in
         // one wave, whose LDS operations run in order, so the row's S reads above
-        // complete before these stores.
+        // complete before these stores.  The S reads are fp32 and the P stores
+        // 16-bit / 128-bit: the compiler barrier keeps type-based alias analysis
+        // from moving the stores above the reads.
+        asm volatile("" ::: "memory");
         {
             uint4 *prow = reinterpret_cast<uint4 *>(Pb + q * PP);
             for (int c = jl; c < Up / 8; c += LPQ) prow[c] = make_uint4(0, 0, 0, 0);
@@ -1359,8 +1365,10 @@ inline int64_t tile_count(const aff_nbhd_attn_args &a) {
     return (int64_t)a.B * ((a.N + tile::TQ - 1) / tile::TQ);
 }
 
-// The wave-per-head kernel: the tile path's conditions, bias modes 0, 2, 4 with
-// table rows that fit its 16-bit codes, at most 256 heads.
+// The wave-per-head kernel: 16-bit q/k/v, head_dim 32, M <= 64, every bias mode,
+// at most MAXH heads and H * M <= MAXHM (its per-(query, neighbour) bias store of
+// TQ * H * M fp32 words is addressed by 16-bit byte offsets), 32-bit offsets inside
+// one image's q/k/v, index and mask planes.
 inline bool use_wave_path(const aff_nbhd_attn_args &a) {
     if (a.dtype == AFF_F32 || a.D != wt::HD || a.M > wt::MAXM) return false;
     if (a.H > wt::MAXH || (int64_t)a.H * a.M > wt::MAXHM) return false;
@@ -1398,6 +1406,13 @@ KernelFn pick_wave(const aff_nbhd_attn_args &a) {
 }  // namespace aff
 
 using namespace aff;
+
+extern "C" int aff_nbhd_attn_path(const aff_nbhd_attn_args *args) {
+    if (args == nullptr) return -1;
+    if (attn::use_wave_path(*args)) return AFF_ATTN_PATH_WAVE;
+    if (attn::use_tile_path(*args)) return AFF_ATTN_PATH_TILE;
+    return AFF_ATTN_PATH_ROW;
+}
 
 extern "C" size_t aff_nbhd_attn_workspace_bytes(const aff_nbhd_attn_args *args) {
     if (args == nullptr || (int64_t)args->B * args->H * args->N == 0) return 0;

@@ -26,11 +26,19 @@ def _as_f32(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
+def _require_2d(D: int) -> None:
+    """The reference accepts D in {2, 3, 4}; only the 2-D search (every model caller's
+    case: token coordinates) is built here."""
+    if D != 2:
+        raise NotImplementedError(f"affmae_amd KNN is built for 2-D coordinates only (got D={D})")
+
+
 def knn_launch(query: torch.Tensor, ref: torch.Tensor, k: int, out_dtype=torch.int32,
                return_dist: bool = False):
     """Call aff_knn on [B,M,2] / [B,N,2] fp32 views; returns idx (and d2)."""
     lib = _lib.load()
     dev = _lib.require_cuda(query, ref)
+    _require_2d(query.shape[-1])
     q = _as_f32(query)
     r = _as_f32(ref)
     B, M, D = q.shape
@@ -61,6 +69,7 @@ def knn_forward(query, ref, k, D=2, use_v2=True, use_heuristic=True):
     assert query.shape[2] == ref.shape[2] == D, f"Expected D={D}, got query D={query.shape[2]}, ref D={ref.shape[2]}"
     assert D in [2, 3, 4], f"D must be 2, 3, or 4, got {D}"
     assert k <= ref.shape[1], f"k={k} exceeds number of reference points N={ref.shape[1]}"
+    _require_2d(D)
     if not use_v2:
         raise ValueError(
             f"use_v2=False is deprecated. Only optimized K=4/K=8 kernels are supported. "
@@ -83,6 +92,7 @@ class KNNFunction(Function):
             assert q.shape[2] == r.shape[2] == D, f"Expected D={D}, got query D={q.shape[2]}, ref D={r.shape[2]}"
             assert D in [2, 3, 4], f"D must be 2, 3, or 4, got {D}"
             assert k <= r.shape[1], f"k={k} exceeds number of reference points N={r.shape[1]}"
+            _require_2d(D)
             # int64 written directly by the kernel (no cast pass)
             return knn_launch(q, r, k, out_dtype=torch.int64)
 
@@ -125,6 +135,7 @@ def knn(query, database, k, return_dist=False, D=None):
     assert query.shape[0] == database.shape[0], "Batch sizes must match"
     assert query.shape[2] == database.shape[2] == D, f"Expected D={D}, got query D={query.shape[2]}, ref D={database.shape[2]}"
     assert k <= database.shape[1], f"k={k} exceeds number of reference points N={database.shape[1]}"
+    _require_2d(D)
     with torch.no_grad():
         idx, d2 = knn_launch(query.detach(), database.detach(), k, out_dtype=torch.int64, return_dist=True)
     return idx, d2.to(query.dtype) if query.dtype != torch.float32 else d2

@@ -13,6 +13,7 @@ a [T*T, H] table by pe_idx, or computed from coordinates in-kernel.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 
 import torch
@@ -23,6 +24,20 @@ from .. import _lib
 from ..utils.pos_embed import REL_POS_WIDTH
 
 _SUPPORTED_D = (8, 16, 32, 64, 128)
+PATH_NAMES = {0: "row", 1: "tile", 2: "wave"}
+_path_log = None
+
+
+@contextlib.contextmanager
+def record_paths():
+    """Collect, in a list, the kernel family ("wave", "tile" or "row") that each
+    aff_nbhd_attn_fwd call inside the block runs (aff_nbhd_attn_path)."""
+    global _path_log
+    prev, _path_log = _path_log, []
+    try:
+        yield _path_log
+    finally:
+        _path_log = prev
 
 
 def _row_ok(t: torch.Tensor) -> bool:
@@ -174,6 +189,8 @@ def nbhd_attn_fwd(q, k, v, member_idx, scale, *, bias=None, pe_idx=None, pe_tabl
 
     a.out, (a.o_sb, a.o_sh, a.o_sn) = out.data_ptr(), out.stride()[:3]
     a.lse = lse.data_ptr() if lse is not None else None
+    if _path_log is not None:
+        _path_log.append(PATH_NAMES.get(int(lib.aff_nbhd_attn_path(ctypes.byref(a))), "?"))
     ws_bytes = int(lib.aff_nbhd_attn_workspace_bytes(ctypes.byref(a)))
     if ws_bytes:
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
@@ -222,4 +239,34 @@ class FlashLocalAttentionFunction(Function):
     @staticmethod
     @custom_bwd(device_type="cuda")
     def backward(ctx, grad_output):
+        raise NotImplementedError("neighbourhood attention backward is not implemented in affmae_amd yet")
+
+
+class ClusterAttnFunction(Function):
+    """Autograd entry of ClusterAttention's local branch.
+
+    forward(q [B,N,H*D], kv [B,N,H*2D], member_idx [B,N,M], pe_idx [B,N,M],
+            table [T*T,H], mask [B,1,N,M] bool or None, blank_k [H,D], blank_v [H,D],
+            scale, H) -> out [B,N,H*D]
+    q is viewed per head as [B,H,N,D]; kv holds each head's [k_h | v_h] pair
+    (the reference's interleave, attention.py:150-152).  The bias of
+    (query, neighbour) is table[pe_idx, h], gathered in-kernel.
+    Gradients are not built yet: backward raises NotImplementedError, so a
+    training step fails loudly instead of running without attention gradients.
+    """
+
+    @staticmethod
+    def forward(ctx, q, kv, member_idx, pe_idx, table, mask, blank_k, blank_v, scale, H):
+        B, N, C = q.shape
+        Ch = C // H
+        qh = q.view(B, N, H, Ch).permute(0, 2, 1, 3)
+        kvh = kv.view(B, N, H, 2 * Ch).permute(0, 2, 1, 3)
+        out = torch.empty((B, N, H, Ch), dtype=q.dtype, device=q.device)
+        nbhd_attn_fwd(qh, kvh[..., :Ch], kvh[..., Ch:], member_idx, scale, pe_idx=pe_idx, pe_table=table,
+                      mask=mask, blank_k=blank_k, blank_v=blank_v, out=out.permute(0, 2, 1, 3),
+                      return_lse=False)
+        return out.view(B, N, C)
+
+    @staticmethod
+    def backward(ctx, grad_out):
         raise NotImplementedError("neighbourhood attention backward is not implemented in affmae_amd yet")

@@ -28,7 +28,7 @@ from ..kernels.fused_deform_attn import (
     fused_knn_deformable_self_attention,
 )
 from ..kernels.knn import knn as hip_knn
-from ..kernels.local_attn import nbhd_attn_fwd
+from ..kernels.local_attn import ClusterAttnFunction
 from ..kernels.msdetrpc import MSDETRPCFunction
 from ..utils.pos_embed import pre_table_fp16, pre_table_fp32
 
@@ -103,20 +103,13 @@ class ClusterAttention(nn.Module):
         if global_attn:
             return self._global(feat, q, kv, pe_idx)
 
-        qh = q.view(B, N, H, Ch).permute(0, 2, 1, 3)                 # [B,H,N,Ch] view
-        kvh = kv.view(B, N, H, 2 * Ch).permute(0, 2, 1, 3)           # [B,H,N,2Ch] view
-        k, v = kvh[..., :Ch], kvh[..., Ch:]
         mask = None
         if cluster_mask is not None:
             mask = (cluster_mask > 0) if cluster_mask.dtype != torch.bool else cluster_mask
             mask = mask.unsqueeze(1)                                  # broadcast over heads
-        out = torch.empty((B, N, H, Ch), dtype=dtype, device=feat.device)
-        nbhd_attn_fwd(qh, k, v, member_idx, self.scale,
-                      pe_idx=pe_idx, pe_table=self.pe_table(dtype),
-                      mask=mask,
-                      blank_k=self.blank_k.view(H, Ch), blank_v=self.blank_v.view(H, Ch),
-                      out=out.permute(0, 2, 1, 3), return_lse=False)
-        out = self.proj(out.view(B, N, C))
+        out = ClusterAttnFunction.apply(q, kv, member_idx, pe_idx, self.pe_table(dtype), mask,
+                                        self.blank_k.view(H, Ch), self.blank_v.view(H, Ch), self.scale, H)
+        out = self.proj(out)
         return self.proj_drop(out)
 
     def _global(self, feat, q, kv, pe_idx):

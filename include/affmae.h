@@ -135,6 +135,16 @@ typedef struct aff_nbhd_attn_args {
 size_t aff_nbhd_attn_workspace_bytes(const aff_nbhd_attn_args *args);
 aff_status aff_nbhd_attn_fwd(const aff_nbhd_attn_args *args, aff_stream_t stream);
 
+/* Which kernel family aff_nbhd_attn_fwd would run for these arguments (no
+ * launch, no validation beyond the path predicates).  A diagnostic with no
+ * counterpart in the reference: tests use it to show which path a case takes.
+ *   AFF_ATTN_PATH_ROW   per-row kernel (any dtype / head_dim)
+ *   AFF_ATTN_PATH_TILE  16-bit MFMA tile kernel plus its flagged-tile pass
+ *   AFF_ATTN_PATH_WAVE  16-bit MFMA wave-per-head kernel
+ * Returns -1 for a NULL pointer. */
+enum { AFF_ATTN_PATH_ROW = 0, AFF_ATTN_PATH_TILE = 1, AFF_ATTN_PATH_WAVE = 2 };
+int aff_nbhd_attn_path(const aff_nbhd_attn_args *args);
+
 /* ------------------------------------------------------------------------ *
  * Weighted neighbour features (the AFF downsampling merge).
  *

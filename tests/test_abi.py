@@ -42,20 +42,24 @@ def test_abi_version(lib):
     assert lib.aff_abi_version() == _lib.ABI_VERSION
 
 
-def test_struct_layout_matches_header(tmp_path):
-    fields = [f for f, _ in _lib.NbhdAttnArgs._fields_]
+@pytest.mark.parametrize("cname,cls", [("aff_nbhd_attn_args", "NbhdAttnArgs"), ("aff_deform_args", "DeformArgs")])
+def test_struct_layout_matches_header(tmp_path, cname, cls):
+    """Size and every field offset of the ctypes mirror equal the C struct's (gcc on the header)."""
+    struct = getattr(_lib, cls)
+    fields = [f for f, _ in struct._fields_]
     src = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void){",
-           'printf("%zu\\n", sizeof(aff_nbhd_attn_args));']
-    src += [f'printf("%zu\\n", offsetof(aff_nbhd_attn_args, {f}));' for f in fields]
+           f'printf("%zu\\n", sizeof({cname}));']
+    src += [f'printf("%zu\\n", offsetof({cname}, {f}));' for f in fields]
     src += ["return 0;}"]
     c = tmp_path / "probe.c"
     c.write_text("\n".join(src))
     exe = tmp_path / "probe"
     subprocess.run(["gcc", str(c), "-o", str(exe)], check=True)
     vals = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
-    assert vals[0] == ctypes.sizeof(_lib.NbhdAttnArgs)
+    assert vals[0] == ctypes.sizeof(struct)
+    assert len(vals) == len(fields) + 1
     for f, off in zip(fields, vals[1:]):
-        assert getattr(_lib.NbhdAttnArgs, f).offset == off, f
+        assert getattr(struct, f).offset == off, f
 
 
 DUMMY = 0x10000  # never dereferenced: validation fails first

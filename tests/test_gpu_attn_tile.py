@@ -1,19 +1,28 @@
-"""MFMA tile path of aff_nbhd_attn_fwd (bf16 / fp16, head_dim 32, M <= 64).
+"""MFMA paths of aff_nbhd_attn_fwd (bf16 / fp16, head_dim 32, M <= 64).
 
-The tile kernel deduplicates the neighbour indices of 16 consecutive queries
-into a union of token rows, runs S^T = K_u Q^T and O = P V_u on the matrix
-cores, and falls back to the per-row routine for tiles whose union is wider
-than 256 rows, whose index window exceeds 8192, whose neighbour lists repeat
-an index, or whose mask differs per head.  Each case below is built so that
-one of those branches runs, and every result is checked against the fp64
-oracle (oracle/oracle.c) at the bf16/fp16 tolerance of 2e-2 max-abs on the
-output and the LSE.
+Two matrix-core kernels serve these calls; aff_nbhd_attn_path() names the one
+a call takes and every test asserts it:
+
+* the wave kernel (H * M <= 192): one workgroup per 32 consecutive queries,
+  one wave per head.  Its set-up deduplicates the tile's neighbour indices
+  into a union of at most 224 token rows; tiles it cannot take (a wider
+  union, an index window over 8192, an index repeated within one query, a
+  per-head mask) run the per-row routine inside the same workgroup.
+* the tile kernel (H * M > 192, e.g. the encoder's 8- and 16-head stages):
+  the same 32-query union, S through LDS and a per-head loop; tiles it
+  cannot take are flagged in the workspace and computed by the flagged-tile
+  pass (nbhd_attn_tile_fallback_kernel) launched right after it.
+
+Each case below is built so that one of those branches runs, and every
+result is checked against the fp64 oracle (oracle/oracle.c) at the
+bf16/fp16 tolerance of 2e-2 max-abs on the output and the LSE.
 """
 import numpy as np
 import pytest
 import torch
 
 from affmae_amd.kernels import knn, nbhd_attn_fwd
+from affmae_amd.kernels.local_attn import record_paths
 from affmae_amd.utils.pos_embed import pre_table_fp32, pe_index
 
 pytestmark = pytest.mark.gpu
@@ -55,11 +64,15 @@ def _qkv(B, H, N, dtype, seed):
     return q, k, v, bk, bv
 
 
-def _run(oracle_mod, dev, q, k, v, idx, scale, dense_bias=None, mask=None, bk=None, bv=None, **kw):
-    print(f"[tile] B,H,N={tuple(q.shape[:3])} M={idx.shape[-1]} {q.dtype} {sorted(kw)}", flush=True)
+def _run(oracle_mod, dev, q, k, v, idx, scale, dense_bias=None, mask=None, bk=None, bv=None, expect=None, **kw):
+    """Run the kernel and the oracle; `expect` ("wave" / "tile") is the path the call must take."""
+    print(f"[tile] B,H,N={tuple(q.shape[:3])} M={idx.shape[-1]} {q.dtype} {sorted(kw)} expect={expect}", flush=True)
     g = lambda t: None if t is None else t.to(dev)
-    out, lse = nbhd_attn_fwd(g(q), g(k), g(v), g(idx), scale, mask=g(mask), blank_k=g(bk), blank_v=g(bv), **kw)
+    with record_paths() as paths:
+        out, lse = nbhd_attn_fwd(g(q), g(k), g(v), g(idx), scale, mask=g(mask), blank_k=g(bk), blank_v=g(bv), **kw)
     torch.cuda.synchronize()
+    if expect is not None:
+        assert paths == [expect], f"expected the {expect} path, ran {paths}"
     ro, rl = oracle_mod.nbhd_attn(_np(q), _np(k), _np(v), idx.cpu().numpy(), scale,
                                   bias=dense_bias, mask=None if mask is None else mask.cpu().numpy(),
                                   blank_k=None if bk is None else _np(bk), blank_v=None if bv is None else _np(bv))
@@ -93,7 +106,8 @@ def test_tile_bias_modes(oracle_mod, dev, dtype, bias_mode):
     elif bias_mode == "continuous":
         dense = oracle_mod.continuous_bias(pos.numpy(), idx.numpy(), w.numpy(), bb.numpy()).astype(np.float32)
         kw = dict(pos=pos.to(dev), pos_weight=w.to(dev), pos_bias=bb.to(dev))
-    out, lse, ro, rl = _run(oracle_mod, dev, q, k, v, idx, 32 ** -0.5, dense_bias=dense, bk=bk, bv=bv, **kw)
+    out, lse, ro, rl = _run(oracle_mod, dev, q, k, v, idx, 32 ** -0.5, dense_bias=dense, bk=bk, bv=bv,
+                            expect="wave", **kw)
     assert out.dtype == dtype
     _check(out, lse, ro, rl, bias_mode)
 
@@ -104,7 +118,7 @@ def test_tile_neighbour_counts(oracle_mod, dev, M):
     pos = _grid_coords(B, N, seed=20 + M)
     idx = knn(pos.to(dev), pos.to(dev), M).cpu() if M else torch.zeros((B, N, 0), dtype=torch.int64)
     q, k, v, bk, bv = _qkv(B, H, N, torch.bfloat16, seed=21)
-    _check(*_run(oracle_mod, dev, q, k, v, idx, 0.3, bk=bk, bv=bv), f"M={M}")
+    _check(*_run(oracle_mod, dev, q, k, v, idx, 0.3, bk=bk, bv=bv, expect="wave"), f"M={M}")
 
 
 @pytest.mark.parametrize("blank", [False, True])
@@ -117,7 +131,7 @@ def test_tile_shared_mask_and_masked_rows(oracle_mod, dev, blank):
     mask = torch.rand((B, 1, N, M), generator=torch.Generator().manual_seed(32)) > 0.3
     mask[:, :, ::5] = False
     out, lse, ro, rl = _run(oracle_mod, dev, q, k, v, idx, 0.3, mask=mask,
-                            bk=bk if blank else None, bv=bv if blank else None)
+                            bk=bk if blank else None, bv=bv if blank else None, expect="wave")
     _check(out, lse, ro, rl, "shared mask")
     if not blank:
         assert torch.all(out[:, :, ::5].float() == 0)
@@ -130,16 +144,16 @@ def test_tile_fallback_repeated_index(oracle_mod, dev):
     idx = knn(pos.to(dev), pos.to(dev), M).cpu()
     idx[:, 7::16, 5] = idx[:, 7::16, 9]          # one query in every tile repeats a neighbour
     q, k, v, bk, bv = _qkv(B, H, N, torch.bfloat16, seed=41)
-    _check(*_run(oracle_mod, dev, q, k, v, idx, 0.3, bk=bk, bv=bv), "repeat")
+    _check(*_run(oracle_mod, dev, q, k, v, idx, 0.3, bk=bk, bv=bv, expect="wave"), "repeat")
 
 
 def test_tile_fallback_wide_union(oracle_mod, dev):
-    """Distinct random neighbours over 4000 tokens: the 16-query union exceeds 256 rows."""
+    """Distinct random neighbours over 4000 tokens: the 32-query union exceeds 224 rows."""
     B, H, N, M = 1, 2, 4000, 48
     g = torch.Generator().manual_seed(50)
     idx = torch.stack([torch.randperm(N, generator=g)[:M] for _ in range(N)]).unsqueeze(0)
     q, k, v, bk, bv = _qkv(B, H, N, torch.float16, seed=51)
-    _check(*_run(oracle_mod, dev, q, k, v, idx, 0.3, bk=bk, bv=bv), "wide union")
+    _check(*_run(oracle_mod, dev, q, k, v, idx, 0.3, bk=bk, bv=bv, expect="wave"), "wide union")
 
 
 def test_tile_fallback_wide_window_mixed(oracle_mod, dev):
@@ -151,7 +165,7 @@ def test_tile_fallback_wide_window_mixed(oracle_mod, dev):
     far = torch.arange(0, 800, 37)
     idx[0, far, 3] = (far + 9000) % N
     q, k, v, bk, bv = _qkv(B, H, N, torch.bfloat16, seed=61)
-    _check(*_run(oracle_mod, dev, q, k, v, idx, 0.3, bk=bk, bv=bv), "wide window")
+    _check(*_run(oracle_mod, dev, q, k, v, idx, 0.3, bk=bk, bv=bv, expect="wave"), "wide window")
 
 
 def test_tile_fallback_per_head_mask(oracle_mod, dev):
@@ -160,7 +174,7 @@ def test_tile_fallback_per_head_mask(oracle_mod, dev):
     idx = knn(pos.to(dev), pos.to(dev), M).cpu()
     q, k, v, bk, bv = _qkv(B, H, N, torch.bfloat16, seed=71)
     mask = torch.rand((B, H, N, M), generator=torch.Generator().manual_seed(72)) > 0.5
-    _check(*_run(oracle_mod, dev, q, k, v, idx, 0.3, mask=mask, bk=bk, bv=bv), "per-head mask")
+    _check(*_run(oracle_mod, dev, q, k, v, idx, 0.3, mask=mask, bk=bk, bv=bv, expect="wave"), "per-head mask")
 
 
 def test_tile_out_of_range_indices(oracle_mod, dev):
@@ -170,7 +184,7 @@ def test_tile_out_of_range_indices(oracle_mod, dev):
     idx[..., 2] = N
     idx[..., 11] = -1
     q, k, v, bk, bv = _qkv(B, H, N, torch.bfloat16, seed=81)
-    _check(*_run(oracle_mod, dev, q, k, v, idx, 0.3, bk=bk, bv=bv), "out of range")
+    _check(*_run(oracle_mod, dev, q, k, v, idx, 0.3, bk=bk, bv=bv, expect="wave"), "out of range")
 
 
 def test_tile_strided_interleaved_kv(oracle_mod, dev):
@@ -193,3 +207,70 @@ def test_tile_strided_interleaved_kv(oracle_mod, dev):
                                  _np(kc[..., :D].contiguous()), _np(kc[..., D:].contiguous()),
                                  idx.cpu().numpy(), 0.25)
     _check(out_buf.permute(0, 2, 1, 3), None, ro, None, "strided")
+
+
+# ---------------------------------------------------------------- tile kernel --
+# H * M > 192: the wave kernel's bias store does not fit, the tile kernel runs.
+
+def _table(H, seed):
+    """[T*T, H] bias table: a seeded Linear(5, H) over the offset features."""
+    g = torch.Generator().manual_seed(seed)
+    w = torch.rand((H, 5), generator=g) * 0.8 - 0.4
+    bb = torch.rand((H,), generator=g) * 0.2 - 0.1
+    return (pre_table_fp32.double() @ w.double().T + bb.double()).float()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("H,M", [(8, 48), (16, 32), (16, 48)])
+@pytest.mark.parametrize("bias_mode", ["table", "coords"])
+def test_tile_kernel_many_heads(oracle_mod, dev, dtype, H, M, bias_mode):
+    """The encoder's 8- and 16-head stages (M = 48, nnc = 6) on integer grid coordinates, as
+    the encoder's tokens are; N = 997 leaves a ragged last tile."""
+    B, N = 2, 997
+    pos = _grid_coords(B, N, seed=100 + H + M).round()
+    idx = knn(pos.to(dev), pos.to(dev), M).cpu()
+    q, k, v, bk, bv = _qkv(B, H, N, dtype, seed=101)
+    table = _table(H, seed=102)
+    pe = pe_index(pos, idx)
+    dense = table[pe].permute(0, 3, 1, 2).contiguous().numpy()
+    kw = dict(pe_idx=pe.to(dev), pe_table=table.to(dev)) if bias_mode == "table" else \
+        dict(pos=pos.to(dev), pe_table=table.to(dev))
+    out, lse, ro, rl = _run(oracle_mod, dev, q, k, v, idx, 32 ** -0.5, dense_bias=dense, bk=bk, bv=bv,
+                            expect="tile", **kw)
+    assert out.dtype == dtype
+    _check(out, lse, ro, rl, f"tile H={H} M={M} {bias_mode}")
+
+
+@pytest.mark.parametrize("case", ["repeat", "wide_union", "per_head_mask", "shared_mask"])
+def test_tile_kernel_flagged_tiles(oracle_mod, dev, case):
+    """Tiles the tile kernel flags (a repeated index, a union over 224 rows, a per-head mask)
+    run in the flagged-tile pass; a shared mask stays on the tile kernel."""
+    B, H, N, M = 1, 8, 640, 48
+    pos = _grid_coords(B, N, seed=110).round()
+    idx = knn(pos.to(dev), pos.to(dev), M).cpu()
+    mask = None
+    if case == "repeat":
+        idx[:, 7::32, 5] = idx[:, 7::32, 9]       # one query in every tile repeats a neighbour
+    elif case == "wide_union":
+        g = torch.Generator().manual_seed(111)
+        far = torch.randint(0, N, (N // 2, M), generator=g)
+        idx[0, 64:64 + N // 2] = far              # tiles 2..11: random neighbours, unions past 224 rows
+    elif case == "per_head_mask":
+        mask = torch.rand((B, H, N, M), generator=torch.Generator().manual_seed(112)) > 0.4
+    else:
+        mask = torch.rand((B, 1, N, M), generator=torch.Generator().manual_seed(113)) > 0.4
+        mask[:, :, ::7] = False
+    q, k, v, bk, bv = _qkv(B, H, N, torch.bfloat16, seed=114)
+    table = _table(H, seed=115)
+    pe = pe_index(pos, idx)
+    dense = table[pe].permute(0, 3, 1, 2).contiguous().numpy()
+    _check(*_run(oracle_mod, dev, q, k, v, idx, 0.3, dense_bias=dense, mask=mask, bk=bk, bv=bv,
+                 expect="tile", pe_idx=pe.to(dev), pe_table=table.to(dev)), f"flagged {case}")
+
+
+def test_tile_kernel_no_bias_no_blank(oracle_mod, dev):
+    B, H, N, M = 2, 16, 300, 24
+    pos = _grid_coords(B, N, seed=120)
+    idx = knn(pos.to(dev), pos.to(dev), M).cpu()
+    q, k, v, _, _ = _qkv(B, H, N, torch.float16, seed=121)
+    _check(*_run(oracle_mod, dev, q, k, v, idx, 0.3, expect="tile"), "tile no bias")
