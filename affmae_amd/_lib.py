@@ -21,6 +21,7 @@ AFF_ERR_WORKSPACE = 3
 AFF_ERR_LAUNCH = 4
 
 AFF_F32, AFF_F16, AFF_BF16 = 0, 1, 2
+KNN_NOALLOC_SCRATCH_BYTES = 16 << 20   # AFF_KNN_NOALLOC_SCRATCH_BYTES
 DTYPE_CODE = {torch.float32: AFF_F32, torch.float16: AFF_F16, torch.bfloat16: AFF_BF16}
 
 ABI_VERSION = 4
@@ -82,6 +83,7 @@ SIGNATURES = {
     "aff_abi_version": (I32, []),
     "aff_knn_workspace_bytes": (SZ, [I32, I32, I32, I32, I32]),
     "aff_knn": (I32, [P, I64, I64, P, I64, I64, I32, I32, I32, I32, I32, P, I32, P, P, SZ, P]),
+    "aff_knn_noalloc": (I32, [P, I64, I64, P, I64, I64, I32, I32, I32, I32, I32, P, I32, P, P]),
     "aff_nbhd_attn_workspace_bytes": (SZ, [ctypes.POINTER(NbhdAttnArgs)]),
     "aff_nbhd_attn_fwd": (I32, [ctypes.POINTER(NbhdAttnArgs), P]),
     "aff_nbhd_attn_path": (I32, [ctypes.POINTER(NbhdAttnArgs)]),

@@ -878,3 +878,68 @@ extern "C" aff_status aff_knn(const float *query, int64_t q_sb, int64_t q_sm, co
     }
     return check_launch("aff_knn/query");
 }
+
+// ------------------------------------------------------------------------
+// aff_knn_noalloc: aff_knn with its workspace in a static device array, for
+// callers that cannot allocate device memory (code under HIP graph capture,
+// serving loops, harnesses that forbid hipMalloc).
+//
+// `scratch` is a file-scope device array: in host code its name is only a
+// host-side stand-in, never a device address.  The device address is taken
+// once per device with hipGetSymbolAddress (with that device current, on the
+// entry point's first call there) and kept per device; only that address is
+// ever handed to kernels.  Every call on one GPU shares that GPU's array: the
+// grid build writes every workspace byte the query kernels read, so nothing
+// has to start at zero, but calls that overlap on one GPU (concurrent streams
+// or host threads) race on it.
+// ------------------------------------------------------------------------
+namespace {
+
+static __device__ __align__(256) unsigned char scratch[AFF_KNN_NOALLOC_SCRATCH_BYTES];
+
+constexpr int SCRATCH_MAXDEV = 64;
+std::once_flag g_scratch_once[SCRATCH_MAXDEV];
+void *g_scratch_ptr[SCRATCH_MAXDEV];
+hipError_t g_scratch_err[SCRATCH_MAXDEV];
+
+// The current device's address of `scratch`.
+aff_status scratch_address(void **out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= SCRATCH_MAXDEV)
+        return fail(AFF_ERR_LAUNCH, "aff_knn_noalloc: no usable current device (%d)", dev);
+    std::call_once(g_scratch_once[dev], [dev] {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        g_scratch_err[dev] = e;
+        g_scratch_ptr[dev] = e == hipSuccess ? p : nullptr;
+    });
+    if (g_scratch_err[dev] != hipSuccess || g_scratch_ptr[dev] == nullptr)
+        return fail(AFF_ERR_LAUNCH, "aff_knn_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                    hipGetErrorString(g_scratch_err[dev]));
+    *out = g_scratch_ptr[dev];
+    return AFF_OK;
+}
+
+}  // namespace
+
+extern "C" aff_status aff_knn_noalloc(const float *query, int64_t q_sb, int64_t q_sm, const float *ref,
+                                      int64_t r_sb, int64_t r_sn, int B, int M, int N, int D, int k,
+                                      void *out_idx, int idx_is_i64, float *out_d2, aff_stream_t stream) {
+    // the argument checks of aff_knn, before the device is touched
+    AFF_CHECK_ARG(B >= 0 && M >= 0, "aff_knn_noalloc: B=%d and M=%d must be >= 0", B, M);
+    AFF_CHECK_ARG(N >= 1, "aff_knn_noalloc: N=%d must be >= 1", N);
+    AFF_CHECK_ARG(k >= 1 && k <= N, "aff_knn_noalloc: k=%d exceeds number of reference points N=%d (or k < 1)", k, N);
+    if (D != 2) return fail(AFF_ERR_UNSUPPORTED, "aff_knn_noalloc: D=%d not supported (only D=2)", D);
+    AFF_CHECK_ARG(q_sb >= 0 && q_sm >= 0 && r_sb >= 0 && r_sn >= 0, "aff_knn_noalloc: negative stride");
+    if (B == 0 || M == 0) return AFF_OK;
+    AFF_CHECK_ARG(query && ref && out_idx, "aff_knn_noalloc: NULL query/ref/out_idx");
+    const size_t need = aff_knn_workspace_bytes(B, M, N, D, k);
+    if (need > (size_t)AFF_KNN_NOALLOC_SCRATCH_BYTES)
+        return fail(AFF_ERR_WORKSPACE, "aff_knn_noalloc: needs %zu bytes of scratch, the static scratch holds %zu",
+                    need, (size_t)AFF_KNN_NOALLOC_SCRATCH_BYTES);
+    void *ws = nullptr;
+    const aff_status st = scratch_address(&ws);
+    if (st != AFF_OK) return st;
+    return aff_knn(query, q_sb, q_sm, ref, r_sb, r_sn, B, M, N, D, k, out_idx, idx_is_i64, out_d2, ws,
+                   (size_t)AFF_KNN_NOALLOC_SCRATCH_BYTES, stream);
+}

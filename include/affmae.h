@@ -66,6 +66,27 @@ aff_status aff_knn(const float *query, int64_t q_sb, int64_t q_sm,
                    void *ws, size_t ws_bytes, aff_stream_t stream);
 
 /* ------------------------------------------------------------------------ *
+ * aff_knn without a caller workspace.
+ *
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): the same search and outputs as aff_knn, with the
+ * workspace taken from a static device array of AFF_KNN_NOALLOC_SCRATCH_BYTES
+ * that each GPU the library runs on holds until the process ends.  Calls
+ * needing more than that (aff_knn_workspace_bytes) fail with
+ * AFF_ERR_WORKSPACE.  Allocates nothing.  All calls on one GPU share its
+ * array: calls that overlap on one GPU (several streams or host threads) race
+ * and must be serialised by the caller.
+ * ------------------------------------------------------------------------ */
+#define AFF_KNN_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+aff_status aff_knn_noalloc(const float *query, int64_t q_sb, int64_t q_sm,
+                           const float *ref, int64_t r_sb, int64_t r_sn,
+                           int B, int M, int N, int D, int k,
+                           void *out_idx, int idx_is_i64, float *out_d2,
+                           aff_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
  * Neighbourhood (cluster) flash attention, forward.
  *
  * Replaces: launch_flash_nbhood_attn_fwd()  src/layers/kernels/local_attn.py:609-708
