@@ -1,3 +1,6 @@
 """nn.Modules with the reference's constructor/forward signatures and parameter names."""
 from .attention import ClusterAttention, DeformableCrossAttention, DeformableSelfAttention  # noqa: F401
-from .aff import ClusterMerging, neighbourhood_index  # noqa: F401
+from .aff import (  # noqa: F401
+    AFFEncoder, AFFPatchEmbed, BasicLayer, ClusterMerging, ClusterTransformerBlock, DropPath, L2NormMerging,
+    LayerNorm2dImages, Mlp, neighbourhood_index,
+)

@@ -49,11 +49,15 @@ class ClusterAttention(nn.Module):
         self.register_buffer('pre_table_fp16', pre_table_fp16.clone())
 
         self.q = nn.Linear(dim, dim)
+        self.q.inp = 'attn'                 # initialisation tags read by AFFEncoder.init_weights
         self.kv = nn.Linear(dim, 2 * dim)
+        self.kv.inp = 'attn'
         self.blank_k = nn.Parameter(torch.randn(dim) * 0.2)
         self.blank_v = nn.Parameter(torch.randn(dim) * 0.2)
         self.pos_embed = nn.Linear(self.pos_dim + 3, num_heads)
+        self.pos_embed.inp = 'norm'
         self.proj = nn.Linear(dim, dim)
+        self.proj.inp = 'norm'
         self.proj_drop = nn.Dropout(proj_drop)
         self._pe_table_cache = {}
 

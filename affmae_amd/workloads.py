@@ -134,3 +134,49 @@ def cfg4(B: int = 32, H: int = 8, C: int = 32, P: int = 4, level_sizes=(6272, 25
     logits = torch.randn((B, Nq, H, L * P), generator=go)
     attn = torch.softmax(logits, dim=-1).reshape(B, Nq, H, L, P).to(dtype)
     return dict(query_pos=qpos, kv_pos=kv_pos, level_start=level_start, values=values, offsets=offsets, attn=attn)
+
+
+def cfg5(B: int = 8, img: int = 1024, patch: int = 4, mask_ratio: float = 0.5, seed: int = 0):
+    """Config 5: B single-channel img x img images ~ N(0, 1) (seed `seed`) and a
+    per-image random patch mask (seed `seed` + 3) with the reference's
+    random_masking semantics (src/utils/masking.py:12-24): the patches are
+    ranked by U(0, 1) noise, the first int(L * (1 - mask_ratio)) of that order
+    are kept (ids_keep, in noise order) and the rest masked (ids_masked).
+    Returns a dict of CPU tensors: images [B,1,img,img] fp32, ids_keep and
+    ids_masked [B, *] int64 over the (img/patch)^2 patch grid."""
+    L = (img // patch) ** 2
+    images = torch.randn((B, 1, img, img), generator=_gen(seed), dtype=torch.float32)
+    noise = torch.rand((B, L), generator=_gen(seed + 3))
+    order = torch.argsort(noise, dim=1)
+    keep = int(L * (1 - mask_ratio))
+    return {"images": images, "ids_keep": order[:, :keep].contiguous(), "ids_masked": order[:, keep:].contiguous()}
+
+
+def mae_encode(encoder, images, ids_keep, ids_masked, patch: int):
+    """The MAE's encoder front end (reference src/models/aff_mae.py:109-134): zero the
+    masked patches of the images, run the masked patch embedding, keep the visible
+    tokens (in ids_keep order) with their grid positions, run the encoder.
+    Returns the encoder's output dict."""
+    B, C, Hh, Ww = images.shape
+    th, tw = Hh // patch, Ww // patch
+    keep = torch.ones((B, th * tw), device=images.device, dtype=images.dtype)
+    keep.scatter_(1, ids_masked, 0.0)
+    keep_map = keep.view(B, 1, th, tw).repeat_interleave(patch, 2).repeat_interleave(patch, 3)
+    pos, feat, h, w = encoder.patch_embed(images * keep_map, ids_masked)
+    vis_feat = feat.gather(1, ids_keep.unsqueeze(-1).expand(-1, -1, feat.shape[-1]))
+    vis_pos = pos.gather(1, ids_keep.unsqueeze(-1).expand(-1, -1, 2))
+    return encoder(vis_feat, vis_pos, h, w)
+
+
+def cfg5_encoder(**overrides):
+    """The AFF-small encoder of config 5: patch 4, dims 64/128/256/512, heads
+    2/4/8/16 (head_dim 32), depths 2/2/6/2, cluster 8, neighbourhood 48 (6
+    nearest clusters), 0.4 weighted-gather (ClusterMerging) downsampling,
+    random init (seed 2), no stochastic depth (inference)."""
+    from .layers.aff import AFFEncoder
+    kw = dict(img_size=1024, patch_size=4, in_chans=1, embed_dims=(64, 128, 256, 512), depths=(2, 2, 6, 2),
+              num_heads=(2, 4, 8, 16), nbhd_sizes=(48, 48, 48, 48), cluster_size=8, ds_rates=(0.4, 0.4, 0.4, 0.4),
+              drop_path_rate=0.0, merging_method="cluster")
+    kw.update(overrides)
+    torch.manual_seed(2)
+    return AFFEncoder(**kw)
