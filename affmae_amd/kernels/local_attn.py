@@ -171,8 +171,8 @@ def nbhd_attn_fwd(q, k, v, member_idx, scale, *, bias=None, pe_idx=None, pe_tabl
             mask = mask.unsqueeze(1)
         assert mask.shape[0] == B and mask.shape[1] in (1, H) and tuple(mask.shape[2:]) == (N, M), \
             f"mask must have shape [batch_size, n_heads, seq_len, neighbor_size] (mask shape: {tuple(mask.shape)})"
-        mk = (mask > 0) if mask.dtype != torch.bool else mask
-        mk = mk.to(torch.uint8)
+        # a bool mask is read as its bytes (0 / 1) without a copy
+        mk = mask.view(torch.uint8) if mask.dtype == torch.bool else (mask > 0).view(torch.uint8)
         if mk.stride(-1) != 1:
             mk = mk.contiguous()
         a.mask = mk.data_ptr()

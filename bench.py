@@ -127,38 +127,155 @@ def other_configs(dev, reps: int):
     res["cfg4_ms_deform_idw"] = {"ms": t_def, "algorithmic_bytes": b4,
                                  "hbm_frac": b4 / (t_def * 1e-3) / HBM_PEAK,
                                  "queries_per_s": 32 * 12544 / (t_def * 1e-3)}
+    del g4, w4
+    res["cfg5_encoder"] = cfg5_encoder(dev, reps)
     return res
 
 
+def cfg5_encoder(dev, reps: int):
+    """Config 5: the AFF-small encoder forward (B=8, 1024^2, patch 4, 32768 visible tokens,
+    bf16 autocast, random init).  Returns images/s of the whole forward and, per stage,
+    the time and HBM fraction of each hot-path kernel call: every call of one forward is
+    recorded (arguments kept), then replayed alone under HIP events."""
+    import torch
+    from affmae_amd import workloads
+    from affmae_amd.layers import aff as aff_mod
+    from affmae_amd.kernels import local_attn
+
+    enc = workloads.cfg5_encoder().to(dev).eval()
+    w5 = workloads.cfg5(B=8, img=1024, seed=0)
+    imgs, keep, masked = w5["images"].to(dev), w5["ids_keep"].to(dev), w5["ids_masked"].to(dev)
+
+    def fwd():
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            return workloads.mae_encode(enc, imgs, keep, masked, 4)
+
+    fwd()
+    t_fwd = time_events(fwd, max(3, reps // 2))
+
+    # one forward with the hot-path entry points wrapped to record their arguments
+    calls = []
+    stage = {"i": -1}
+    orig = (aff_mod.knn, aff_mod.weighted_features, local_attn.nbhd_attn_fwd)
+
+    def rec_knn(q, r, k, *a, **kw):
+        stage["i"] += 1
+        calls.append(("knn", stage["i"], (q, r, k)))
+        return orig[0](q, r, k, *a, **kw)
+
+    def rec_wf(wts, feat, idx):
+        calls.append(("merge", stage["i"], (wts, feat, idx)))
+        return orig[1](wts, feat, idx)
+
+    def rec_attn(*a, **kw):
+        calls.append(("attn", stage["i"], (a, kw)))
+        return orig[2](*a, **kw)
+
+    aff_mod.knn, aff_mod.weighted_features, local_attn.nbhd_attn_fwd = rec_knn, rec_wf, rec_attn
+    try:
+        fwd()
+    finally:
+        aff_mod.knn, aff_mod.weighted_features, local_attn.nbhd_attn_fwd = orig
+    torch.cuda.synchronize()
+
+    el = lambda t: t.numel() * t.element_size()
+    stages = [dict(n=0, attn_ms=0.0, attn_calls=0, attn_bytes=0, knn_ms=0.0, merge_ms=0.0, merge_bytes=0)
+              for _ in range(4)]
+    for kind, si, args in calls:
+        st = stages[si]
+        if kind == "knn":
+            q, r, k = args
+            st["n"] = q.shape[1]
+            st["knn_ms"] += time_events(lambda: orig[0](q, r, k), reps)
+        elif kind == "merge":
+            wts, feat, idx = args
+            t = time_events(lambda: orig[1](wts, feat, idx), reps)
+            B5, n2, M5, IC = wts.shape
+            st["merge_ms"] += t
+            # weights, indices and the source features in, [B, n', IC, C] out (every tensor once)
+            st["merge_bytes"] += el(wts) + el(idx) + el(feat) + B5 * n2 * IC * feat.shape[-1] * feat.element_size()
+        else:
+            a, kw = args
+            t = time_events(lambda: orig[2](*a, **kw), reps)
+            q, kk, v, mi = a[0], a[1], a[2], a[3]
+            mask, table, pe = kw.get("mask"), kw.get("pe_table"), kw.get("pe_idx")
+            by = 4 * el(q) + el(mi) + (el(pe) if pe is not None else 0) + (el(table) if table is not None else 0)
+            if mask is not None:
+                by += mask.numel()                        # read as uint8
+            st["attn_ms"] += t
+            st["attn_calls"] += 1
+            st["attn_bytes"] += by
+            st["heads"] = q.shape[1]
+    out = {"ms": t_fwd, "images_per_s": 8 / (t_fwd * 1e-3), "tokens_per_s": 8 * 32768 / (t_fwd * 1e-3),
+           "hot_path_ms": sum(s_["attn_ms"] + s_["knn_ms"] + s_["merge_ms"] for s_ in stages), "stages": []}
+    for i, st in enumerate(stages):
+        e = {"tokens": st["n"], "heads": st.get("heads"), "attn_calls": st["attn_calls"],
+             "attn_ms": st["attn_ms"], "knn_ms": st["knn_ms"], "merge_ms": st["merge_ms"]}
+        if st["attn_ms"] > 0:
+            e["attn_hbm_frac"] = st["attn_bytes"] / (st["attn_ms"] * 1e-3) / HBM_PEAK
+        if st["merge_ms"] > 0:
+            e["merge_hbm_frac"] = st["merge_bytes"] / (st["merge_ms"] * 1e-3) / HBM_PEAK
+        out["stages"].append(e)
+    out["hot_path_frac_of_forward"] = out["hot_path_ms"] / t_fwd
+    return out
+
+
+def host_cpu() -> dict:
+    """CPU model, physical cores and logical CPUs of this host, and the CPUs this process may use."""
+    model, cores = "unknown", set()
+    phys = core = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "model name" and model == "unknown":
+                model = v
+            elif k == "physical id":
+                phys = v
+            elif k == "core id":
+                core = v
+            elif not k and phys is not None and core is not None:
+                cores.add((phys, core))
+                phys = core = None
+    except OSError:
+        pass
+    return {"model": model, "physical_cores": len(cores) or None, "logical_cpus": os.cpu_count(),
+            "usable_cpus": len(os.sched_getaffinity(0))}
+
+
 def cpu_baseline(w, table_cpu, budget_s: float):
-    """Oracle KNN + fp64 oracle attention on whole images until the budget is spent."""
-    import numpy as np
-    import oracle
+    """The reference's own PyTorch path on this host's CPU, fp32, per image until the budget is
+    spent: knn_pytorch_large (cdist^2 + topk, knn.py:1312-1332), the table bias gather
+    (attention.py:117-124) and the gathered softmax attention (local_attn.py:979-1006)."""
+    import torch
+    from oracle import torch_path
     from affmae_amd.utils.pos_embed import pe_index
 
-    oracle.lib()
-    threads = oracle.num_threads()
-    pos = w["pos"].numpy()
-    q, k, v = (w[n].float().numpy() for n in ("q", "k", "v"))
-    bk, bv = w["blank_k"].float().numpy(), w["blank_v"].float().numpy()
-    tab = table_cpu.numpy()
+    threads = torch.get_num_threads()
+    pos = w["pos"]
+    q, k, v = (w[n].float() for n in ("q", "k", "v"))
+    bk, bv = w["blank_k"].float(), w["blank_v"].float()
     done, t_total = 0, 0.0
-    while done < B and (t_total < budget_s or done == 0):
-        b = done
-        t0 = time.perf_counter()
-        idx, _ = oracle.knn(pos[b:b + 1], pos[b:b + 1], K_NN)
-        pe = oracle.pe_index(pos[b:b + 1], idx)
-        dense = oracle.table_bias(pe, tab)
-        oracle.nbhd_attn(q[b:b + 1], k[b:b + 1], v[b:b + 1], idx, D ** -0.5, bias=dense, blank_k=bk, blank_v=bv)
-        t_total += time.perf_counter() - t0
-        done += 1
+    with torch.no_grad():
+        while done < B and (t_total < budget_s or done == 0):
+            b = done
+            t0 = time.perf_counter()
+            idx = torch_path.knn_cdist_topk(pos[b:b + 1], pos[b:b + 1], K_NN)
+            bias = torch_path.table_bias(pe_index(pos[b:b + 1], idx), table_cpu)
+            torch_path.gathered_attention(q[b:b + 1], k[b:b + 1], v[b:b + 1], idx, D ** -0.5, bias=bias,
+                                          blank_k=bk, blank_v=bv)
+            t_total += time.perf_counter() - t0
+            done += 1
+    host = host_cpu()
     return {
         "value": done * N / t_total,
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{done} of {B} images ({done * N} tokens): oracle KNN k=48 (fp32, exact) + "
-                  f"fp64 neighbourhood attention, {t_total:.2f} s on {threads} OpenMP threads",
+        "sample": f"{done} of {B} images ({done * N} tokens) of the reference's PyTorch path in torch-CPU fp32: "
+                  f"cdist^2+topk KNN k=48, table bias gather, gathered softmax attention with blank token; "
+                  f"{t_total:.2f} s on {threads} torch threads",
+        "host": host,
     }
 
 

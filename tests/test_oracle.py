@@ -450,3 +450,31 @@ def test_cluster_members_out_of_range(oracle_mod):
     mo, ko, _ = oracle_mod.cluster_members(nearest, members, np.ones((1, 3, 2), np.int64))
     assert mo.tolist() == [[[1, 0, 0, 0], [0, 0, 0, 1]]]
     assert ko.tolist() == [[[1, 0, 0, 0], [0, 0, 1, 1]]]
+
+
+# ------------------------------------------- torch-CPU baseline (bench.py) --
+def test_torch_path_matches_oracle(oracle_mod):
+    """oracle/torch_path.py (the reference's own PyTorch path, timed as bench.py's CPU
+    baseline) agrees with the C oracle: the cdist+topk KNN selects the oracle's sets
+    on tie-free inputs, and the gathered attention with table bias, mask and blank
+    token is within fp32 rounding of the fp64 oracle."""
+    import torch
+    from oracle import torch_path
+    rng = np.random.default_rng(7)
+    B, N, H, D, M = 2, 400, 2, 32, 24
+    pos = rng.random((B, N, 2), dtype=np.float32) * 40
+    idx_o, _ = oracle_mod.knn(pos, pos, M)
+    idx_t = torch_path.knn_cdist_topk(torch.from_numpy(pos), torch.from_numpy(pos), M).numpy()
+    assert np.array_equal(np.sort(idx_t, -1), np.sort(idx_o, -1))
+    q, k, v = (rng.standard_normal((B, H, N, D)).astype(np.float32) for _ in range(3))
+    bk, bv = (rng.standard_normal((H, D)).astype(np.float32) * 0.3 for _ in range(2))
+    table = (oracle_mod.pre_table().astype(np.float64) @ rng.uniform(-0.3, 0.3, (H, 5)).T).astype(np.float32)
+    pe = oracle_mod.pe_index(np.floor(pos), idx_o)
+    mask = rng.random((B, 1, N, M)) > 0.2
+    ro, _ = oracle_mod.nbhd_attn(q, k, v, idx_o, D ** -0.5, bias=oracle_mod.table_bias(pe, table), mask=mask,
+                                 blank_k=bk, blank_v=bv)
+    t = torch.from_numpy
+    bias = torch_path.table_bias(t(pe), t(table))
+    out = torch_path.gathered_attention(t(q), t(k), t(v), t(idx_o), D ** -0.5, bias=bias, mask=t(mask),
+                                        blank_k=t(bk), blank_v=t(bv)).numpy()
+    assert np.abs(out - ro).max() <= 1e-5 * np.abs(ro).max()
