@@ -57,6 +57,19 @@ class NbhdAttnArgs(ctypes.Structure):
     ]
 
 
+class NbhdAttnBwdArgs(ctypes.Structure):
+    """Mirror of ``aff_nbhd_attn_bwd_args`` (include/affmae.h)."""
+    _fields_ = [
+        ("fwd", NbhdAttnArgs),
+        ("dout", P), ("do_sb", I64), ("do_sh", I64), ("do_sn", I64),
+        ("dq", P), ("dq_sb", I64), ("dq_sh", I64), ("dq_sn", I64),
+        ("dk", P), ("dk_sb", I64), ("dk_sh", I64), ("dk_sn", I64),
+        ("dv", P), ("dv_sb", I64), ("dv_sh", I64), ("dv_sn", I64),
+        ("dbias", P), ("dtable", P), ("dblank_k", P), ("dblank_v", P),
+        ("ws", P), ("ws_bytes", SZ),
+    ]
+
+
 DEFORM_MAX_LEVELS = 8
 DEFORM_SHEPARD, DEFORM_IDW = 0, 1
 
@@ -87,6 +100,8 @@ SIGNATURES = {
     "aff_nbhd_attn_workspace_bytes": (SZ, [ctypes.POINTER(NbhdAttnArgs)]),
     "aff_nbhd_attn_fwd": (I32, [ctypes.POINTER(NbhdAttnArgs), P]),
     "aff_nbhd_attn_path": (I32, [ctypes.POINTER(NbhdAttnArgs)]),
+    "aff_nbhd_attn_bwd_workspace_bytes": (SZ, [ctypes.POINTER(NbhdAttnBwdArgs)]),
+    "aff_nbhd_attn_bwd": (I32, [ctypes.POINTER(NbhdAttnBwdArgs), P]),
     "aff_weighted_features_fwd": (I32, [P, I32, I64, I64, I64, I64, P, I32, I64, I64, P, I32, I64, I64,
                                         I32, I32, I32, I32, I32, I32, P, I64, I64, I64, P]),
     "aff_weighted_gather_fwd": (I32, [P, I32, I64, I64, P, I32, I64, I64, P, I32, I64, I64,

@@ -66,25 +66,10 @@ def _idx(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
-def nbhd_attn_fwd(q, k, v, member_idx, scale, *, bias=None, pe_idx=None, pe_table=None,
-                  pos=None, pos_weight=None, pos_bias=None, rel_width=REL_POS_WIDTH, mask=None,
-                  blank_k=None, blank_v=None, out=None, return_lse=True):
-    """Neighbourhood attention forward through aff_nbhd_attn_fwd.
-
-    q, k, v   : [B,H,N,D] (any strides with a unit stride on D), one dtype
-    member_idx: [B,N,M] int32/int64
-    bias      : dense [B,H,N,M], or
-    pe_idx + pe_table: bias[b,h,n,j] = pe_table[pe_idx[b,n,j], h], or
-    pos + pe_table: as above with pe_idx computed in-kernel from the
-                coordinates exactly as the encoder does (aff.py:458-465), or
-    pos + pos_weight [H,5] + pos_bias [H]: continuous relative-position bias
-    mask      : [B,1|H,N,M] (nonzero = valid) or None
-    blank_k/v : [H,D] or None
-    out       : optional [B,H,N,D] view to write into (e.g. a [B,N,H,D] buffer
-                permuted), otherwise allocated contiguous [B,H,N,D]
-    Returns (out, lse [B,H,N] fp32 or None).
-    """
-    lib = _lib.load()
+def _attn_args(q, k, v, member_idx, scale, *, bias=None, pe_idx=None, pe_table=None, pos=None, pos_weight=None,
+               pos_bias=None, rel_width=REL_POS_WIDTH, mask=None, blank_k=None, blank_v=None):
+    """Validate the inputs and fill an aff_nbhd_attn_args (no out / lse / workspace yet).
+    Returns (args, keep, device): keep holds every tensor the args point into."""
     dev = _lib.require_cuda(q, k, v, member_idx, bias, pe_idx, pe_table, pos, mask, blank_k, blank_v)
     dtype = q.dtype
     if dtype not in _lib.DTYPE_CODE:
@@ -99,11 +84,6 @@ def nbhd_attn_fwd(q, k, v, member_idx, scale, *, bias=None, pe_idx=None, pe_tabl
     k = _prep_qkv(k, dtype)
     v = _prep_qkv(v, dtype)
     mi = _idx(member_idx)
-    if out is None:
-        out = torch.empty((B, H, N, D), dtype=dtype, device=dev)
-    else:
-        assert tuple(out.shape) == (B, H, N, D) and out.dtype == dtype and _row_ok(out), "bad out view"
-    lse = torch.empty((B, H, N), dtype=torch.float32, device=dev) if return_lse else None
 
     a = _lib.NbhdAttnArgs()
     a.dtype = _lib.DTYPE_CODE[dtype]
@@ -115,8 +95,7 @@ def nbhd_attn_fwd(q, k, v, member_idx, scale, *, bias=None, pe_idx=None, pe_tabl
     a.member_idx = mi.data_ptr()
     a.idx_is_i64 = 1 if mi.dtype == torch.int64 else 0
     a.mi_sb, a.mi_sn = mi.stride(0), mi.stride(1)
-    keep = [q, k, v, mi, out]
-
+    keep = [q, k, v, mi]
     if bias is not None and bias.numel() > 0:
         assert tuple(bias.shape) == (B, H, N, M), \
             "bias must have shape [batch_size, n_heads, seq_len, neighbor_size]"
@@ -187,6 +166,39 @@ def nbhd_attn_fwd(q, k, v, member_idx, scale, *, bias=None, pe_idx=None, pe_tabl
         a.blank_k, a.blank_v = bk.data_ptr(), bv.data_ptr()
         keep += [bk, bv]
 
+    return a, keep, dev
+
+
+def nbhd_attn_fwd(q, k, v, member_idx, scale, *, bias=None, pe_idx=None, pe_table=None,
+                  pos=None, pos_weight=None, pos_bias=None, rel_width=REL_POS_WIDTH, mask=None,
+                  blank_k=None, blank_v=None, out=None, return_lse=True):
+    """Neighbourhood attention forward through aff_nbhd_attn_fwd.
+
+    q, k, v   : [B,H,N,D] (any strides with a unit stride on D), one dtype
+    member_idx: [B,N,M] int32/int64
+    bias      : dense [B,H,N,M], or
+    pe_idx + pe_table: bias[b,h,n,j] = pe_table[pe_idx[b,n,j], h], or
+    pos + pe_table: as above with pe_idx computed in-kernel from the
+                coordinates exactly as the encoder does (aff.py:458-465), or
+    pos + pos_weight [H,5] + pos_bias [H]: continuous relative-position bias
+    mask      : [B,1|H,N,M] (nonzero = valid) or None
+    blank_k/v : [H,D] or None
+    out       : optional [B,H,N,D] view to write into (e.g. a [B,N,H,D] buffer
+                permuted), otherwise allocated contiguous [B,H,N,D]
+    Returns (out, lse [B,H,N] fp32 or None).
+    """
+    lib = _lib.load()
+    a, keep, dev = _attn_args(q, k, v, member_idx, scale, bias=bias, pe_idx=pe_idx, pe_table=pe_table, pos=pos,
+                              pos_weight=pos_weight, pos_bias=pos_bias, rel_width=rel_width, mask=mask,
+                              blank_k=blank_k, blank_v=blank_v)
+    dtype = q.dtype
+    B, H, N, D = q.shape
+    if out is None:
+        out = torch.empty((B, H, N, D), dtype=dtype, device=dev)
+    else:
+        assert tuple(out.shape) == (B, H, N, D) and out.dtype == dtype and _row_ok(out), "bad out view"
+    lse = torch.empty((B, H, N), dtype=torch.float32, device=dev) if return_lse else None
+    keep.append(out)
     a.out, (a.o_sb, a.o_sh, a.o_sn) = out.data_ptr(), out.stride()[:3]
     a.lse = lse.data_ptr() if lse is not None else None
     if _path_log is not None:
@@ -200,6 +212,68 @@ def nbhd_attn_fwd(q, k, v, member_idx, scale, *, bias=None, pe_idx=None, pe_tabl
     _lib.check(st, "aff_nbhd_attn_fwd")
     del keep
     return out, lse
+
+
+def nbhd_attn_bwd(dout, q, k, v, member_idx, scale, out, lse, *, bias=None, pe_idx=None, pe_table=None, pos=None,
+                  rel_width=REL_POS_WIDTH, mask=None, blank_k=None, blank_v=None, dq=None, dk=None, dv=None,
+                  want_dbias=False, want_dtable=False):
+    """Gradients of nbhd_attn_fwd through aff_nbhd_attn_bwd (reference local_attn.py:711-840).
+
+    The inputs are the forward's (same bias form), plus its output `out` and
+    `lse` and the upstream gradient `dout` [B,H,N,D].  dq / dk / dv may be
+    given as [B,H,N,D] views to write into (e.g. the per-head slices of a
+    projection's gradient), otherwise they are allocated.  Returns
+    (dq, dk, dv, dbias [B,H,N,M] fp32 or None, dtable [rows,H] fp32 or None,
+    dblank_k [H,D] fp32 or None, dblank_v [H,D] fp32 or None).  Every sum is
+    formed in a fixed order, so the result is bitwise reproducible.
+    """
+    lib = _lib.load()
+    a, keep, dev = _attn_args(q, k, v, member_idx, scale, bias=bias, pe_idx=pe_idx, pe_table=pe_table, pos=pos,
+                              rel_width=rel_width, mask=mask, blank_k=blank_k, blank_v=blank_v)
+    dtype = q.dtype
+    B, H, N, D = q.shape
+    M = member_idx.shape[-1]
+    o = _prep_qkv(out, dtype)
+    ls = lse.to(torch.float32).contiguous()
+    do = _prep_qkv(dout, dtype)
+    a.out, (a.o_sb, a.o_sh, a.o_sn) = o.data_ptr(), o.stride()[:3]
+    a.lse = ls.data_ptr()
+    keep += [o, ls, do]
+
+    def grad_buf(t):
+        if t is None:
+            return torch.empty((B, H, N, D), dtype=dtype, device=dev)
+        assert tuple(t.shape) == (B, H, N, D) and t.dtype == dtype and _row_ok(t), "bad gradient view"
+        return t
+
+    dq, dk, dv = grad_buf(dq), grad_buf(dk), grad_buf(dv)
+    g = _lib.NbhdAttnBwdArgs()
+    g.fwd = a
+    g.dout, (g.do_sb, g.do_sh, g.do_sn) = do.data_ptr(), do.stride()[:3]
+    g.dq, (g.dq_sb, g.dq_sh, g.dq_sn) = dq.data_ptr(), dq.stride()[:3]
+    g.dk, (g.dk_sb, g.dk_sh, g.dk_sn) = dk.data_ptr(), dk.stride()[:3]
+    g.dv, (g.dv_sb, g.dv_sh, g.dv_sn) = dv.data_ptr(), dv.stride()[:3]
+    dbias = torch.empty((B, H, N, M), dtype=torch.float32, device=dev) if want_dbias else None
+    dtable = None
+    if want_dtable:
+        assert a.bias_mode in (2, 4), "dtable needs a table bias (pe_idx or pos with pe_table)"
+        dtable = torch.empty((int(a.table_rows), H), dtype=torch.float32, device=dev)
+    dbk = dbv = None
+    if a.blank_k:
+        dbk = torch.empty((H, D), dtype=torch.float32, device=dev)
+        dbv = torch.empty((H, D), dtype=torch.float32, device=dev)
+    g.dbias = dbias.data_ptr() if dbias is not None else None
+    g.dtable = dtable.data_ptr() if dtable is not None else None
+    g.dblank_k = dbk.data_ptr() if dbk is not None else None
+    g.dblank_v = dbv.data_ptr() if dbv is not None else None
+    ws_bytes = int(lib.aff_nbhd_attn_bwd_workspace_bytes(ctypes.byref(g)))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    g.ws, g.ws_bytes = ws.data_ptr(), ws_bytes
+    keep.append(ws)
+    st = lib.aff_nbhd_attn_bwd(ctypes.byref(g), _lib.stream_ptr(dev))
+    _lib.check(st, "aff_nbhd_attn_bwd")
+    del keep
+    return dq, dk, dv, dbias, dtable, dbk, dbv
 
 
 def launch_flash_nbhood_attn_fwd(q, k, v, member_index, sm_scale, bias=None, mask=None,
@@ -225,21 +299,31 @@ class FlashLocalAttentionFunction(Function):
     """Autograd entry point (reference local_attn.py:843-936).
 
     forward(Q, K, V, member_idx, bias, mask, blank_k, blank_v, softmax_scale)
-    -> [B,H,N,D] in Q's dtype.  The backward kernels are not built yet and
-    raise NotImplementedError.
+    -> [B,H,N,D] in Q's dtype; backward returns (dQ, dK, dV, None, dbias,
+    None, dblank_k, dblank_v, None) like the reference, from aff_nbhd_attn_bwd.
     """
 
     @staticmethod
     @custom_fwd(device_type="cuda")
     def forward(ctx, Q, K, V, member_idx, bias, mask, blank_k, blank_v, softmax_scale):
-        out, _ = launch_flash_nbhood_attn_fwd(Q, K, V, member_idx, softmax_scale, bias=bias, mask=mask,
-                                              blank_k=blank_k, blank_v=blank_v)
+        out, lse = launch_flash_nbhood_attn_fwd(Q, K, V, member_idx, softmax_scale, bias=bias, mask=mask,
+                                                blank_k=blank_k, blank_v=blank_v)
+        ctx.save_for_backward(Q, K, V, member_idx, bias, mask, blank_k, blank_v, out, lse)
+        ctx.scale = softmax_scale
         return out
 
     @staticmethod
     @custom_bwd(device_type="cuda")
     def backward(ctx, grad_output):
-        raise NotImplementedError("neighbourhood attention backward is not implemented in affmae_amd yet")
+        Q, K, V, member_idx, bias, mask, blank_k, blank_v, out, lse = ctx.saved_tensors
+        has_bias = bias is not None and bias.numel() > 0
+        has_blank = blank_k is not None and blank_v is not None and blank_k.numel() > 0
+        dq, dk, dv, dbias, _, dbk, dbv = nbhd_attn_bwd(
+            grad_output, Q, K, V, member_idx, ctx.scale, out, lse, bias=bias if has_bias else None, mask=mask,
+            blank_k=blank_k if has_blank else None, blank_v=blank_v if has_blank else None,
+            want_dbias=has_bias and ctx.needs_input_grad[4])
+        return (dq, dk, dv, None, dbias.to(bias.dtype) if dbias is not None else None, None,
+                dbk.to(blank_k.dtype) if has_blank else None, dbv.to(blank_v.dtype) if has_blank else None, None)
 
 
 class ClusterAttnFunction(Function):
@@ -250,9 +334,9 @@ class ClusterAttnFunction(Function):
             scale, H) -> out [B,N,H*D]
     q is viewed per head as [B,H,N,D]; kv holds each head's [k_h | v_h] pair
     (the reference's interleave, attention.py:150-152).  The bias of
-    (query, neighbour) is table[pe_idx, h], gathered in-kernel.
-    Gradients are not built yet: backward raises NotImplementedError, so a
-    training step fails loudly instead of running without attention gradients.
+    (query, neighbour) is table[pe_idx, h], gathered in-kernel.  backward
+    returns dq, dkv (written straight into the projections' layouts), dtable
+    and the blank tokens' gradients from aff_nbhd_attn_bwd.
     """
 
     @staticmethod
@@ -262,11 +346,30 @@ class ClusterAttnFunction(Function):
         qh = q.view(B, N, H, Ch).permute(0, 2, 1, 3)
         kvh = kv.view(B, N, H, 2 * Ch).permute(0, 2, 1, 3)
         out = torch.empty((B, N, H, Ch), dtype=q.dtype, device=q.device)
-        nbhd_attn_fwd(qh, kvh[..., :Ch], kvh[..., Ch:], member_idx, scale, pe_idx=pe_idx, pe_table=table,
-                      mask=mask, blank_k=blank_k, blank_v=blank_v, out=out.permute(0, 2, 1, 3),
-                      return_lse=False)
+        need = any(ctx.needs_input_grad)
+        _, lse = nbhd_attn_fwd(qh, kvh[..., :Ch], kvh[..., Ch:], member_idx, scale, pe_idx=pe_idx, pe_table=table,
+                               mask=mask, blank_k=blank_k, blank_v=blank_v, out=out.permute(0, 2, 1, 3),
+                               return_lse=need)
+        if need:
+            ctx.save_for_backward(q, kv, member_idx, pe_idx, table, mask, blank_k, blank_v, out, lse)
+            ctx.scale, ctx.H = scale, H
         return out.view(B, N, C)
 
     @staticmethod
     def backward(ctx, grad_out):
-        raise NotImplementedError("neighbourhood attention backward is not implemented in affmae_amd yet")
+        q, kv, member_idx, pe_idx, table, mask, blank_k, blank_v, out, lse = ctx.saved_tensors
+        B, N, C = q.shape
+        H = ctx.H
+        Ch = C // H
+        heads = lambda t, w: t.view(B, N, H, w).permute(0, 2, 1, 3)
+        dq = torch.empty_like(q)
+        dkv = torch.empty_like(kv)
+        kvh, dkvh = heads(kv, 2 * Ch), heads(dkv, 2 * Ch)
+        _, _, _, _, dtable, dbk, dbv = nbhd_attn_bwd(
+            grad_out.to(q.dtype).reshape(B, N, H, Ch).permute(0, 2, 1, 3), heads(q, Ch), kvh[..., :Ch], kvh[..., Ch:], member_idx, ctx.scale,
+            out.permute(0, 2, 1, 3), lse, pe_idx=pe_idx, pe_table=table, mask=mask, blank_k=blank_k,
+            blank_v=blank_v, dq=heads(dq, Ch), dk=dkvh[..., :Ch], dv=dkvh[..., Ch:],
+            want_dtable=ctx.needs_input_grad[4])
+        return (dq, dkv, None, None, dtable.to(table.dtype) if dtable is not None else None, None,
+                dbk.to(blank_k.dtype) if dbk is not None else None, dbv.to(blank_v.dtype) if dbv is not None else None,
+                None, None)

@@ -167,6 +167,54 @@ enum { AFF_ATTN_PATH_ROW = 0, AFF_ATTN_PATH_TILE = 1, AFF_ATTN_PATH_WAVE = 2 };
 int aff_nbhd_attn_path(const aff_nbhd_attn_args *args);
 
 /* ------------------------------------------------------------------------ *
+ * Neighbourhood (cluster) flash attention, backward.
+ *
+ * Replaces: launch_flash_nbhood_attn_bwd()  src/layers/kernels/local_attn.py:711-840
+ *           kernels _nbhood_attn_bwd_preprocess / _nbhood_attn_bwd_internal
+ *           local_attn.py:350-606 (FlashLocalAttentionFunction.backward :911-936)
+ *
+ * With Delta = sum_d out * dout over each (b, h, n) row (out = the forward
+ * output), and for every valid neighbour j of the row (valid as in the
+ * forward; masked and out-of-range neighbours get no gradient):
+ *   p_j  = exp(s_j - lse),  s_j = scale <q, k_j> + bias_j
+ *   dS_j = p_j (<dout, v_j> - Delta)
+ *   dq   = scale (sum_j dS_j k_j + dS_blank blank_k)
+ *   dk[idx_j] += scale dS_j q,   dv[idx_j] += p_j dout
+ *   dbias[b, h, n, j] = dS_j
+ *   dtable[row_j, h] += dS_j  (bias modes 2 and 4: row_j the table row the forward read)
+ *   dblank_k[h] += scale dS_blank q,  dblank_v[h] += p_blank dout
+ * The scattered sums are formed without floating-point atomics, each in a
+ * fixed order (the (b, n, j) order of the contributing pairs), so the
+ * result is bitwise reproducible.
+ *
+ * fwd: the forward call's arguments; fwd.out must be the forward output and
+ * fwd.lse its LSE (both required); fwd.ws is not used.  Bias modes 0, 1, 2
+ * and 4 (mode 3 returns AFF_ERR_UNSUPPORTED).
+ * dout / dq / dk / dv: [B, H, N, D] in fwd.dtype with element strides and a
+ * unit stride on D (16-byte aligned rows).  dk / dv rows no pair points at
+ * are written as zeros.
+ * dbias: [B, H, N, M] fp32 contiguous, or NULL.  dtable: [table_rows, H] fp32
+ * contiguous (modes 2 and 4), or NULL.  dblank_k / dblank_v: [H, D] fp32,
+ * both set (when the forward had blank tokens) or both NULL.
+ * ws: aff_nbhd_attn_bwd_workspace_bytes() bytes, 256-byte aligned.
+ * ------------------------------------------------------------------------ */
+typedef struct aff_nbhd_attn_bwd_args {
+    aff_nbhd_attn_args fwd;
+    const void *dout; int64_t do_sb, do_sh, do_sn;
+    void *dq; int64_t dq_sb, dq_sh, dq_sn;
+    void *dk; int64_t dk_sb, dk_sh, dk_sn;
+    void *dv; int64_t dv_sb, dv_sh, dv_sn;
+    float *dbias;
+    float *dtable;
+    float *dblank_k;
+    float *dblank_v;
+    void *ws; size_t ws_bytes;
+} aff_nbhd_attn_bwd_args;
+
+size_t aff_nbhd_attn_bwd_workspace_bytes(const aff_nbhd_attn_bwd_args *args);
+aff_status aff_nbhd_attn_bwd(const aff_nbhd_attn_bwd_args *args, aff_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
  * Weighted neighbour features (the AFF downsampling merge).
  *
  * Replaces: weighted_features() / WeightedFeaturesFunction

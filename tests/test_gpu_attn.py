@@ -293,18 +293,3 @@ def test_cluster_attention_module(oracle_mod, dev, with_mask):
     err = float((out - ref).abs().max())
     assert err <= 1e-5 * max(scale, 1.0), f"rel err {err / scale:.3e}"
 
-
-def test_cluster_attention_backward_raises(dev):
-    """With gradients enabled the local branch runs through an autograd Function; until the
-    backward kernels exist its backward must raise instead of dropping the gradients."""
-    from affmae_amd.layers import ClusterAttention
-    B, N, C, H, M = 1, 256, 64, 2, 16
-    pos = torch.floor(workloads.cfg1_coords(B, N, seed=7) * 16).to(dev)
-    idx = knn(pos, pos, M)
-    pe = pe_index(pos.cpu(), idx.cpu()).to(dev)
-    m = ClusterAttention(C, H).to(dev).train()
-    feat = torch.randn((B, N, C), device=dev, requires_grad=True)
-    out = m(feat, idx, None, pe, False)
-    assert out.requires_grad and out.grad_fn is not None
-    with pytest.raises(NotImplementedError):
-        out.sum().backward()

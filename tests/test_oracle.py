@@ -478,3 +478,28 @@ def test_torch_path_matches_oracle(oracle_mod):
     out = torch_path.gathered_attention(t(q), t(k), t(v), t(idx_o), D ** -0.5, bias=bias, mask=t(mask),
                                         blank_k=t(bk), blank_v=t(bv)).numpy()
     assert np.abs(out - ro).max() <= 1e-5 * np.abs(ro).max()
+
+
+def test_torch_path_gradients_match_finite_differences():
+    """The fp64 autograd gradients of oracle/torch_path.gathered_attention, which the GPU
+    backward tests use as their reference, agree with central finite differences for every
+    input the kernel differentiates (q, k, v, the table bias, blank_k, blank_v), with a
+    mask and a repeated neighbour index."""
+    import torch
+    from oracle import torch_path
+    g = torch.Generator().manual_seed(3)
+    B, H, N, D, M = 1, 2, 7, 4, 3
+    q, k, v = (torch.randn((B, H, N, D), generator=g, dtype=torch.float64, requires_grad=True) for _ in range(3))
+    idx = torch.randint(0, N, (B, N, M), generator=g)
+    idx[0, 2, 1] = idx[0, 2, 0]                                  # a repeated neighbour
+    table = torch.randn((10, H), generator=g, dtype=torch.float64, requires_grad=True)
+    pe = torch.randint(0, 10, (B, N, M), generator=g)
+    mask = torch.ones((B, 1, N, M), dtype=torch.bool)
+    mask[0, 0, 4, 2] = False
+    bk, bv = (torch.randn((H, D), generator=g, dtype=torch.float64, requires_grad=True) for _ in range(2))
+
+    def f(q, k, v, table, bk, bv):
+        bias = torch_path.table_bias(pe, table)
+        return torch_path.gathered_attention(q, k, v, idx, 0.7, bias=bias, mask=mask, blank_k=bk, blank_v=bv)
+
+    assert torch.autograd.gradcheck(f, (q, k, v, table, bk, bv), eps=1e-6, atol=1e-7, rtol=1e-5)
