@@ -104,6 +104,9 @@ SIGNATURES = {
     "aff_nbhd_attn_bwd": (I32, [ctypes.POINTER(NbhdAttnBwdArgs), P]),
     "aff_weighted_features_fwd": (I32, [P, I32, I64, I64, I64, I64, P, I32, I64, I64, P, I32, I64, I64,
                                         I32, I32, I32, I32, I32, I32, P, I64, I64, I64, P]),
+    "aff_weighted_features_bwd_workspace_bytes": (SZ, [I32, I32, I32, I32]),
+    "aff_weighted_features_bwd": (I32, [P, I64, I64, I64, P, I32, I64, I64, I64, I64, P, I32, I64, I64, P, I32,
+                                        I64, I64, I32, I32, I32, I32, I32, I32, P, I32, P, P, SZ, P]),
     "aff_weighted_gather_fwd": (I32, [P, I32, I64, I64, P, I32, I64, I64, P, I32, I64, I64,
                                       I32, I32, I32, I32, I32, P, I64, I64, P]),
     "aff_softmax_merge_fwd": (I32, [P, I64, I64, P, I64, I64, P, I32, I64, I64, P, I32, I64, I64,

@@ -15,10 +15,9 @@
 // 1. bwd_rows_kernel, one (b, h, n) row per D/8 lanes: recomputes s_j, p_j,
 //    <dout, v_j> and dS_j, writes dq, and keeps p_j and dS_j of every
 //    (row, neighbour) pair (and the blank token's p and dS per row).
-// 2. The pairs are bucketed by the key row they point at: keys (b * N +
-//    idx_j) with payload (b * N + n) * M + j go through a stable radix sort
-//    (hipCUB), so each key row's incoming pairs are listed in (b, n, j) order,
-//    and a lower_bound per key gives the bucket offsets.
+// 2. The pairs are bucketed by the key row they point at (bucket.hpp): keys
+//    (b * N + idx_j) with payload (b * N + n) * M + j, stably sorted, so each
+//    key row's incoming pairs are listed in (b, n, j) order.
 // 3. bwd_keys_kernel, one (b, h, key row) per D/8 lanes: walks its bucket in
 //    order and accumulates dk = scale * sum dS q_n and dv = sum p dout_n.
 // 4. Bias modes 2 / 4: the pairs are bucketed again by table row and
@@ -29,7 +28,7 @@
 #include "common.hpp"
 #include "nbhd_attn_common.hpp"
 
-#include <hipcub/device/device_radix_sort.hpp>
+#include "bucket.hpp"
 
 namespace aff {
 namespace attn_bwd {
@@ -232,19 +231,6 @@ __global__ __launch_bounds__(THREADS) void table_keys_kernel(const aff_nbhd_attn
     vals[e] = int(e);
 }
 
-// off[k] = first position of key >= k in the sorted keys, k = 0 .. nkeys.
-__global__ __launch_bounds__(THREADS) void bucket_offsets_kernel(const unsigned *keys, int64_t count, int nkeys, int *off) {
-    const int k = blockIdx.x * THREADS + threadIdx.x;
-    if (k > nkeys) return;
-    int64_t lo = 0, hi = count;
-    while (lo < hi) {
-        const int64_t mid = (lo + hi) >> 1;
-        if (keys[mid] < unsigned(k)) lo = mid + 1;
-        else hi = mid;
-    }
-    off[k] = int(lo);
-}
-
 // ------------------------------------------------------------- key pass --
 template <typename T, int D>
 __global__ __launch_bounds__(THREADS) void bwd_keys_kernel(const aff_nbhd_attn_bwd_args g, const float *P,
@@ -409,20 +395,6 @@ struct BwdLayout {
     size_t temp_bytes;
 };
 
-inline int key_bits(int64_t max_key) {
-    int bits = 1;
-    while (bits < 31 && ((int64_t)1 << bits) <= max_key) ++bits;
-    return bits;
-}
-
-inline size_t sort_temp_bytes(int64_t count, int bits) {
-    size_t bytes = 0;
-    hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, static_cast<const unsigned *>(nullptr), static_cast<unsigned *>(nullptr),
-                                       static_cast<const int *>(nullptr), static_cast<int *>(nullptr), (int)count, 0,
-                                       bits, (hipStream_t)0);
-    return bytes;
-}
-
 inline bool wants_table(const aff_nbhd_attn_bwd_args &g) {
     return g.dtable != nullptr && (g.fwd.bias_mode == 2 || g.fwd.bias_mode == 4);
 }
@@ -447,9 +419,9 @@ inline BwdLayout layout(const aff_nbhd_attn_bwd_args &g) {
     L.vals_out = take(sizeof(int) * pairs);
     L.off_kv = take(sizeof(int) * ((int64_t)a.B * a.N + 1));
     L.off_tab = wants_table(g) ? take(sizeof(int) * (a.table_rows + 1)) : 0;
-    size_t tb = sort_temp_bytes(pairs, key_bits((int64_t)a.B * a.N));
+    size_t tb = bucket::sort_temp_bytes(pairs, bucket::key_bits((int64_t)a.B * a.N));
     if (wants_table(g)) {
-        const size_t t2 = sort_temp_bytes(pairs, key_bits(a.table_rows));
+        const size_t t2 = bucket::sort_temp_bytes(pairs, bucket::key_bits(a.table_rows));
         tb = t2 > tb ? t2 : tb;
     }
     L.temp_bytes = tb;
@@ -596,14 +568,10 @@ extern "C" aff_status aff_nbhd_attn_bwd(const aff_nbhd_attn_bwd_args *args, aff_
     if (pairs > 0) {
         hipLaunchKernelGGL(kv_keys_kernel, dim3(blocks_for(pairs, THREADS)), dim3(THREADS), 0, hs, a, keys_in, vals_in);
         if ((s = check_launch("aff_nbhd_attn_bwd (keys)")) != AFF_OK) return s;
-        size_t tb = L.temp_bytes;
-        if (hipcub::DeviceRadixSort::SortPairs(ws + L.temp, tb, keys_in, keys_out, vals_in, vals_out, (int)pairs, 0,
-                                               key_bits(nkv), hs) != hipSuccess)
-            return fail(AFF_ERR_LAUNCH, "aff_nbhd_attn_bwd: radix sort of the key rows failed");
     }
-    hipLaunchKernelGGL(bucket_offsets_kernel, dim3(blocks_for((int64_t)nkv + 1, THREADS)), dim3(THREADS), 0, hs,
-                       keys_out, pairs, nkv, off_kv);
-    if ((s = check_launch("aff_nbhd_attn_bwd (offsets)")) != AFF_OK) return s;
+    if ((s = bucket::sort_and_offsets(keys_in, vals_in, keys_out, vals_out, pairs, nkv, ws + L.temp, L.temp_bytes,
+                                      off_kv, hs)) != AFF_OK)
+        return s;
     const KeysFn keys_fn = by_dtype(dt, pick_keys<float>(D), pick_keys<bf16_t>(D), pick_keys<f16_t>(D));
     hipLaunchKernelGGL(keys_fn, dim3(blocks_for(rows, rows_per_block)), dim3(THREADS), 0, hs, g, P, dS, vals_out, off_kv);
     if ((s = check_launch("aff_nbhd_attn_bwd (key rows)")) != AFF_OK) return s;
@@ -616,14 +584,10 @@ extern "C" aff_status aff_nbhd_attn_bwd(const aff_nbhd_attn_bwd_args *args, aff_
             hipLaunchKernelGGL(a.bias_mode == 2 ? table_keys_kernel<2> : table_keys_kernel<4>,
                                dim3(blocks_for(pairs, THREADS)), dim3(THREADS), 0, hs, a, keys_in, vals_in);
             if ((s = check_launch("aff_nbhd_attn_bwd (table keys)")) != AFF_OK) return s;
-            size_t tb = L.temp_bytes;
-            if (hipcub::DeviceRadixSort::SortPairs(ws + L.temp, tb, keys_in, keys_out, vals_in, vals_out, (int)pairs, 0,
-                                                   key_bits(tr), hs) != hipSuccess)
-                return fail(AFF_ERR_LAUNCH, "aff_nbhd_attn_bwd: radix sort of the table rows failed");
         }
-        hipLaunchKernelGGL(bucket_offsets_kernel, dim3(blocks_for((int64_t)tr + 1, THREADS)), dim3(THREADS), 0, hs,
-                           keys_out, pairs, tr, off_tab);
-        if ((s = check_launch("aff_nbhd_attn_bwd (table offsets)")) != AFF_OK) return s;
+        if ((s = bucket::sort_and_offsets(keys_in, vals_in, keys_out, vals_out, pairs, tr, ws + L.temp, L.temp_bytes,
+                                          off_tab, hs)) != AFF_OK)
+            return s;
         hipLaunchKernelGGL(table_grad_kernel, dim3(blocks_for(tr, THREADS / 64)), dim3(THREADS), 0, hs, a, dS, vals_out,
                            off_tab, g.dtable);
         if ((s = check_launch("aff_nbhd_attn_bwd (table rows)")) != AFF_OK) return s;

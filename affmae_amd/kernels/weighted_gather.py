@@ -17,6 +17,7 @@ from torch.amp import custom_fwd, custom_bwd
 
 from .. import _lib
 from .knn import knn_launch
+from .weighted_features import weighted_features_backward
 
 
 def _idx(t):
@@ -53,18 +54,24 @@ def launch_weighted_gather_fwd_kernel(nbhd_idx, weights, feat, out=None):
 
 
 class WeightedGatherFunction(torch.autograd.Function):
-    """Autograd entry (forward only: the backward kernels are not built yet)."""
+    """Autograd entry (reference weighted_gather.py:329-361): backward returns
+    (None, d_weights, d_feat), the IC = 1 case of aff_weighted_features_bwd."""
 
     @staticmethod
     @custom_fwd(device_type="cuda")
     def forward(ctx, nbhd_idx, weights, feat):
         assert nbhd_idx.is_cuda and weights.is_cuda and feat.is_cuda, "All inputs must be CUDA tensors."
+        ctx.save_for_backward(nbhd_idx, weights, feat)
         return launch_weighted_gather_fwd_kernel(nbhd_idx, weights, feat)
 
     @staticmethod
     @custom_bwd(device_type="cuda")
     def backward(ctx, dout):
-        raise NotImplementedError("weighted_gather backward is not implemented in affmae_amd yet")
+        nbhd_idx, weights, feat = ctx.saved_tensors
+        dw, df = weighted_features_backward(dout.unsqueeze(2), weights.unsqueeze(-1), feat, nbhd_idx,
+                                            need_weights=ctx.needs_input_grad[1], need_feat=ctx.needs_input_grad[2])
+        return (None, dw.squeeze(-1).to(weights.dtype) if dw is not None else None,
+                df.to(feat.dtype) if df is not None else None)
 
 
 def weighted_gather(nbhd_idx: torch.Tensor, weights: torch.Tensor, feat: torch.Tensor) -> torch.Tensor:

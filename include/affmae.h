@@ -237,6 +237,35 @@ aff_status aff_weighted_features_fwd(const void *weights, int w_dtype, int64_t w
                                      aff_stream_t stream);
 
 /* ------------------------------------------------------------------------ *
+ * Weighted neighbour features, backward.
+ *
+ * Replaces: WeightedFeaturesFunction.backward  src/layers/kernels/weighted_features.py:421-430,
+ *           kernels :164-398; WeightedGatherFunction.backward (weighted_gather.py:349-361,
+ *           kernels :127-326) as the IC = 1 case.
+ *
+ *   d_weights[b, i, m, ic] = sum_c dout[b, i, ic, c] * feat[b, idx[b, i, m], c]
+ *   d_feat[b, r, c] = sum over (i, m) with idx[b, i, m] = r of
+ *                     sum_ic weights[b, i, m, ic] * dout[b, i, ic, c]
+ * dout [B, Nout, IC, C] in f_dtype (strides do_sb, do_sn, do_sic; unit stride
+ * on C); weights / feat / nbhd_idx as in the forward.  d_weights: [B, Nout, M,
+ * IC] contiguous in dw_dtype, or NULL; d_feat: [B, Nsrc, C] contiguous in
+ * f_dtype, or NULL.  Indices outside [0, Nsrc) contribute nothing and get
+ * d_weights 0.  IC <= 8.  d_feat is a fixed-order sum (the (b, i, m) order of
+ * the entries), with no atomics: bitwise reproducible.  ws:
+ * aff_weighted_features_bwd_workspace_bytes(B, Nout, Nsrc, M) bytes, 256-byte
+ * aligned (only needed for d_feat).
+ * ------------------------------------------------------------------------ */
+size_t aff_weighted_features_bwd_workspace_bytes(int B, int Nout, int Nsrc, int M);
+aff_status aff_weighted_features_bwd(const void *dout, int64_t do_sb, int64_t do_sn, int64_t do_sic,
+                                     const void *weights, int w_dtype, int64_t w_sb, int64_t w_sn,
+                                     int64_t w_sm, int64_t w_sic,
+                                     const void *feat, int f_dtype, int64_t f_sb, int64_t f_sn,
+                                     const void *nbhd_idx, int idx_is_i64, int64_t i_sb, int64_t i_sn,
+                                     int B, int Nout, int Nsrc, int M, int C, int IC,
+                                     void *d_weights, int dw_dtype, void *d_feat,
+                                     void *ws, size_t ws_bytes, aff_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
  * Weighted gather: the IC = 1 case of the above.
  *
  * Replaces: weighted_gather() / WeightedGatherFunction
