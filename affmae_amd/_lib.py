@@ -24,7 +24,7 @@ AFF_F32, AFF_F16, AFF_BF16 = 0, 1, 2
 KNN_NOALLOC_SCRATCH_BYTES = 16 << 20   # AFF_KNN_NOALLOC_SCRATCH_BYTES
 DTYPE_CODE = {torch.float32: AFF_F32, torch.float16: AFF_F16, torch.bfloat16: AFF_BF16}
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 P = ctypes.c_void_p
 I32 = ctypes.c_int

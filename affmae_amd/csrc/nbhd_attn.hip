@@ -6,33 +6,11 @@
 // blank token joins the softmax after the neighbours, the running maximum
 // starts at -1e11 and LSE = m + log(l + 1e-12).
 //
-// Three kernels implement it; the host picks the first that takes the call.
+// Two kernels implement it; the host picks the first that takes the call.
 //
-// nbhd_attn_wave_kernel (bf16 / fp16, head_dim 32, M <= 64, H * M <= 192):
-// one wave per head over a 32-query tile, described where it is defined.
-//
-// nbhd_attn_tile_kernel (bf16 / fp16, head_dim 32, M <= 64, any H): one workgroup
-// takes 32 consecutive queries of one image and every head.  The tile's
-// neighbour indices are deduplicated into a "union" of at most 224 token
-// rows (an LDS bitmap over the tile's index window plus a popcount prefix
-// gives every (query, neighbour) pair a union slot).  Per head the union's
-// K rows feed S^T = K_u Q^T on v_mfma_f32_16x16x32 (K straight from HBM/L2
-// into the A operand, Q as the B operand), S goes to LDS, the softmax runs
-// in (query, neighbour) layout - 8 lanes per query, one entry per neighbour
-// and lane, logits in log2 units - and the probabilities are scattered into a
-// dense P[32 x U] tile, zero where a query does not use a union row.
-// O = P V_u is a second MFMA pass with V rows staged in LDS as they are and
-// read column-wise by gfx950's transposing LDS reads, each wave owning one
-// 16 x 16 output block.  Every K/V row the tile touches is read
-// once per head instead of once per (query, neighbour), and both contractions
-// run on the matrix cores.  The next head's K/V/Q/bias loads are issued as
-// soon as the current head's K/V registers are consumed (after its S MFMAs
-// and V^T stores), so their latency overlaps its softmax, PV pass and store.
-// A tile whose union exceeds 224 rows, whose index window exceeds 8192, whose
-// neighbour lists repeat an index within one query, or whose mask differs per
-// head is flagged in the caller's workspace (one byte per tile) and computed
-// by nbhd_attn_tile_fallback_kernel, launched right after on the same stream,
-// with the per-row routine below.
+// nbhd_attn_wave_kernel (bf16 / fp16, head_dim 32, M <= 64, any H and bias
+// mode): one workgroup per (32-query tile, head group), one wave per head;
+// described where it is defined.
 //
 // nbhd_attn_fwd_kernel (every dtype and head_dim, the rest): D/8 lanes own one
 // (b, h, n) row (8 channels each).  Neighbours are consumed 8 at a time:
@@ -214,55 +192,6 @@ __global__ __launch_bounds__(THREADS) void nbhd_attn_fwd_kernel(const aff_nbhd_a
     attend_row<T, D, BIAS, 8>(a, int(bh / a.H), int(bh % a.H), n, sub);
 }
 
-// ------------------------------------------------------------------------
-// MFMA tile kernel
-// ------------------------------------------------------------------------
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-template <typename T> struct Mfma;
-template <> struct Mfma<bf16_t> {
-    typedef __bf16 v8 __attribute__((ext_vector_type(8)));
-    __device__ __forceinline__ static f32x4 mma(uint4 a, uint4 b, f32x4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0,
-                                                       0, 0);
-    }
-    __device__ __forceinline__ static uint16_t from_f32(float x) { return f32_to_bf16(x); }
-    __device__ __forceinline__ static float to_f32(uint16_t x) { return bf16_to_f32(x); }
-};
-template <> struct Mfma<f16_t> {
-    typedef _Float16 v8 __attribute__((ext_vector_type(8)));
-    __device__ __forceinline__ static f32x4 mma(uint4 a, uint4 b, f32x4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0, 0,
-                                                      0);
-    }
-    __device__ __forceinline__ static uint16_t from_f32(float x) { return __builtin_bit_cast(uint16_t, _Float16(x)); }
-    __device__ __forceinline__ static float to_f32(uint16_t x) { return float(__builtin_bit_cast(_Float16, x)); }
-};
-
-namespace tile {
-constexpr int TQ = 32;               // queries per workgroup (two 16-row MFMA blocks)
-constexpr int HD = 32;               // head_dim of this kernel
-constexpr int UMAX = 224;            // union rows held in LDS
-constexpr int WWORDS = 256;          // index-window bitmap words: windows up to 8192 indices
-constexpr int MAXM = 64;             // neighbours per query
-constexpr int LPQ = 8;               // lanes per query in the softmax
-constexpr int RJ = MAXM / LPQ;       // neighbour entries per lane: j = jl + 8 r
-constexpr int KBW = (UMAX / 16 + 3) / 4;                  // 16-slot K blocks per wave
-constexpr int PCV = (UMAX * 4 + THREADS - 1) / THREADS;  // 16-byte V row pieces per thread
-constexpr int SP = UMAX + 4;         // S row pitch (fp32): 16-byte rows, 4-bank shift per row
-constexpr int PP = 2 * SP;           // P row pitch (16-bit): P row q overwrites S row q in place;
-                                     // column UMAX (inside the row) is a dummy
-constexpr int VRP = 40;              // V row pitch (16-bit): 80-byte rows
-constexpr int OP = HD + 4;           // O row pitch (fp32)
-constexpr float LOG2E = 1.4426950408889634f;
-static_assert(WWORDS == THREADS, "one bitmap word per thread");
-static_assert(TQ * LPQ == THREADS, "one softmax lane group per query");
-static_assert(UMAX % 32 == 0, "union rows come in 32-row MFMA chunks");
-}  // namespace tile
-
-__device__ __forceinline__ uint4 ld16(const char *p) { return *reinterpret_cast<const uint4 *>(p); }
-__device__ __forceinline__ uint2 ld8(const char *p) { return *reinterpret_cast<const uint2 *>(p); }
-
 // ds_read_b64_tr_b16: within each group of 16 lanes, lane 4a + b receives
 // element b of the four 16-bit values addressed by lanes a, 4 + a, 8 + a and
 // 12 + a (in that order).  With lane 4k + a pointing at row s_k, columns
@@ -288,451 +217,6 @@ __device__ __forceinline__ float grp8_sum(float v) {
     return v + dpp_mov<0x141>(v);
 }
 
-// One workgroup (4 waves) per 32-query tile of one image, every head.
-// flags[tile] = 0 when the tile ran here, 1 when it must take the per-row
-// fallback (union wider than UMAX rows, index window wider than 8192, an index
-// repeated within one query's list, or a per-head mask).
-//
-// Per head:  S^T = K_u Q^T on v_mfma_f32_16x16x32 (wave w: 16-slot blocks
-// w, w + 4, ...; both query halves share the K operand), S -> LDS; softmax
-// with 8 lanes x RJ entries per query reading S at the entries' union slots,
-// logits pre-scaled by log2(e) so one v_exp_f32 per entry; P (16-bit) to a
-// dense [query][slot] tile written over the query's own S row (non-member
-// slots 0); O = P V_u with V rows in
-// LDS, wave w owning output block (query half w & 1, channel half w >> 1);
-// normalise, add the blank value, store.  The next head's Q/K/V/bias loads
-// are issued once this head's K/V registers are consumed.
-template <typename T, int BIAS>
-__global__ __launch_bounds__(THREADS) void nbhd_attn_tile_kernel(const aff_nbhd_attn_args a, int ntiles) {
-    using namespace tile;
-    using MM = Mfma<T>;
-    struct SetupLds {
-        uint32_t bits[WWORDS];
-        uint32_t pref[WWORDS];
-    };
-    __shared__ __align__(16) union {
-        SetupLds s;
-        float S[TQ * SP];        // scores, then (per row, in place) the 16-bit probabilities
-        uint16_t P[TQ * PP];
-    } sh;
-    uint16_t *const Pb = sh.P;
-    __shared__ __align__(16) uint16_t Vs[UMAX * VRP];
-    // the union list and the per-query slot bits are only used while setting
-    // up the tile, O only in the head loop: they share one region
-    struct UnionLds {
-        int ulist[UMAX];
-        uint32_t qbits[TQ][UMAX / 32];
-    };
-    __shared__ __align__(16) union {
-        UnionLds u;
-        float Ob[TQ * OP];
-    } sh2;
-    int *const ulist = sh2.u.ulist;
-    auto &qbits = sh2.u.qbits;
-    float *const Ob = sh2.Ob;
-    __shared__ float linfo[TQ][2];
-    __shared__ int red[4];
-
-    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    const int q = t >> 3, jl = t & 7;  // softmax role: query q, entries jl + 8 r
-    const int N = a.N, M = a.M, H = a.H;
-    const int tiles = (N + TQ - 1) / TQ;
-    const int rowq = lane & 15, grp = lane >> 4;
-    uint8_t *flags = static_cast<uint8_t *>(a.ws);
-    const int tile = int(xcd_swizzle(blockIdx.x, gridDim.x));
-    const int b = tile / tiles;
-    const int n0 = (tile % tiles) * TQ;
-    const int n = n0 + q;
-    const bool qlive = n < N;
-    const int nc = min(n, N - 1);
-
-    if (t < 4) red[t] = 0;
-    sh.s.bits[t] = 0;
-    for (int i = t; i < TQ * UMAX / 32; i += THREADS) (&qbits[0][0])[i] = 0;
-
-    // ---- this lane's (query, neighbour) entries.  With a mask, the head-0 row
-    // is every head's row (a per-head mask sends the tile to the fallback).
-    const int64_t mi_row = (int64_t)b * a.mi_sb + (int64_t)nc * a.mi_sn;
-    const int64_t mk_row = (int64_t)b * a.mask_sb + (int64_t)nc * a.mask_sn;
-    int idx[RJ];
-    bool use[RJ];
-    int nmask = 0;
-#pragma unroll
-    for (int r = 0; r < RJ; ++r) {
-        const int j = jl + LPQ * r;
-        const bool live = qlive && j < M;
-        const int64_t ix = live ? load_index(a.member_idx, a.idx_is_i64, mi_row + j) : -1;
-        bool ok = live && ix >= 0 && ix < N;
-        if (ok && a.mask) ok = a.mask[mk_row + j] != 0;
-        use[r] = ok;
-        idx[r] = ok ? int(ix) : 0;
-        nmask += (live && !ok) ? 1 : 0;
-    }
-    // coordinate terms of the bias, shared by every head (modes 2-4): issued
-    // here, consumed after the union is built, so they overlap its LDS work
-    float gx_[RJ], gy_[RJ];
-    int64_t gpe[RJ];
-    float pqx = 0.f, pqy = 0.f;
-#pragma unroll
-    for (int r = 0; r < RJ; ++r) {
-        gx_[r] = gy_[r] = 0.f;
-        gpe[r] = -1;
-    }
-    if constexpr (BIAS == 2) {
-#pragma unroll
-        for (int r = 0; r < RJ; ++r)
-            if (use[r])
-                gpe[r] = load_index(a.pe_idx, a.pe_is_i64, (int64_t)b * a.pe_sb + (int64_t)nc * a.pe_sn + jl + LPQ * r);
-    } else if constexpr (BIAS == 3 || BIAS == 4) {
-        const float *pos_b = a.pos + (int64_t)b * a.pos_sb;
-        pqx = pos_b[(int64_t)nc * a.pos_sn];
-        pqy = pos_b[(int64_t)nc * a.pos_sn + 1];
-#pragma unroll
-        for (int r = 0; r < RJ; ++r)
-            if (use[r]) {
-                gx_[r] = pos_b[(int64_t)idx[r] * a.pos_sn];
-                gy_[r] = pos_b[(int64_t)idx[r] * a.pos_sn + 1];
-            }
-    }
-
-    // the cleared bitmap and counters are visible before any wave's atomics
-    lds_barrier();
-
-    // ---- union of the tile's neighbour rows over the index window
-    // [wlo, wlo + 8192) around the tile (every index when N <= 8192)
-    const int wlo = max(0, min(n0 + TQ / 2 - WWORDS * 16, N - WWORDS * 32));
-    bool outside = false;
-#pragma unroll
-    for (int r = 0; r < RJ; ++r)
-        if (use[r]) {
-            const unsigned o = unsigned(idx[r] - wlo);
-            if (o < unsigned(WWORDS * 32)) atomicOr(&sh.s.bits[o >> 5], 1u << (o & 31));
-            else outside = true;
-        }
-    if (outside) red[0] = 1;
-    lds_barrier();
-    if ((a.mask && a.mask_sh != 0) || red[0]) {
-        if (t == 0) flags[tile] = 1;
-        return;
-    }
-    if (w == 0) {
-        uint32_t c[4];
-        int tot = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            c[i] = __popc(sh.s.bits[lane * 4 + i]);
-            tot += c[i];
-        }
-        int inc = tot;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int v = __shfl_up(inc, o, 64);
-            if (lane >= o) inc += v;
-        }
-        int ex = inc - tot;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            sh.s.pref[lane * 4 + i] = ex;
-            ex += c[i];
-        }
-        if (lane == 63) red[2] = inc;
-    }
-    lds_barrier();
-    const int U = red[2];
-    if (U > UMAX) {
-        if (t == 0) flags[tile] = 1;
-        return;
-    }
-    int slot[RJ];
-#pragma unroll
-    for (int r = 0; r < RJ; ++r) {
-        slot[r] = UMAX;  // the dummy column
-        if (use[r]) {
-            const int o = idx[r] - wlo, wd = o >> 5, bt = o & 31;
-            const int s = int(sh.s.pref[wd] + __popc(sh.s.bits[wd] & ((1u << bt) - 1u)));
-            slot[r] = s;
-            ulist[s] = idx[r];
-            const uint32_t bit = 1u << (s & 31);
-            if (atomicOr(&qbits[q][s >> 5], bit) & bit) red[3] = 1;  // repeated index
-        }
-    }
-    lds_barrier();
-    if (red[3]) {
-        if (t == 0) flags[tile] = 1;
-        return;
-    }
-    if (t == 0) flags[tile] = 0;
-
-    // bias terms from the gathered coordinates / pe indices
-    float fx[RJ], fy[RJ];
-    int tab[RJ];
-#pragma unroll
-    for (int r = 0; r < RJ; ++r) {
-        fx[r] = fy[r] = 0.f;
-        tab[r] = -1;
-        if constexpr (BIAS == 2) {
-            if (use[r]) tab[r] = (gpe[r] >= 0 && gpe[r] < a.table_rows) ? int(gpe[r]) : -1;
-        } else if constexpr (BIAS == 4) {
-            if (use[r]) {
-                const int64_t v = pe_from_coords(pqx, pqy, gx_[r], gy_[r], float(a.rel_width),
-                                                 float(2 * a.rel_width + 1));
-                tab[r] = (v >= 0 && v < a.table_rows) ? int(v) : -1;
-            }
-        } else if constexpr (BIAS == 3) {
-            fx[r] = gx_[r] - pqx;
-            fy[r] = gy_[r] - pqy;
-        }
-    }
-
-    const int Up = (U + 31) & ~31;
-    const int nkb = Up >> 4, nkb2 = Up >> 5;
-    const bool blank = a.blank_k != nullptr;
-    const float scale2 = a.scale * LOG2E;
-    const float nmq = grp8_sum(float(nmask));  // masked (live) entries of this query
-
-    // ---- per-lane byte offsets into one head's planes, the same for every head
-    // (the host guarantees they fit in 32 bits).  Union slots past U read the
-    // first union row for K (their S columns are never read) and zero for V.
-    const int row0 = U > 0 ? ulist[0] : 0;
-    const uint32_t ksn2 = uint32_t(a.k_sn * 2), vsn2 = uint32_t(a.v_sn * 2);  // < 2^24, host-checked
-    uint32_t koff[KBW];
-#pragma unroll
-    for (int i = 0; i < KBW; ++i) {
-        const int s = (w + 4 * i) * 16 + rowq;
-        koff[i] = __umul24(uint32_t(s < U ? ulist[s] : row0), ksn2) + grp * 16;
-    }
-    // V row pieces: piece pc = t + 256 i is row pc >> 2, channels 8 (pc & 3) .. +8
-    uint32_t voff[PCV];
-#pragma unroll
-    for (int i = 0; i < PCV; ++i) {
-        const int pc = t + THREADS * i, s = pc >> 2, dc = pc & 3;
-        voff[i] = __umul24(uint32_t(s < U ? ulist[s] : row0), vsn2) + dc * 16;
-    }
-    // softmax entries: LDS byte offsets of S[q][slot] and P[q][slot]
-    uint32_t sadr[RJ], padr[RJ];
-#pragma unroll
-    for (int r = 0; r < RJ; ++r) {
-        sadr[r] = uint32_t((q * SP + slot[r]) * 4);
-        padr[r] = uint32_t((q * PP + slot[r]) * 2);
-    }
-    const int trk = (lane & 15) >> 2, tra = lane & 3;  // transposing-read role: row k, columns 4a
-    uint32_t qoff[2];
-#pragma unroll
-    for (int qh = 0; qh < 2; ++qh)
-        qoff[qh] = uint32_t(((int64_t)min(n0 + 16 * qh + rowq, N - 1) * a.q_sn + grp * 8) * 2);
-    const uint32_t qboff = uint32_t(((int64_t)nc * a.q_sn + 4 * jl) * 2);  // blank logit: channels 4 jl .. +4
-    const float *table = static_cast<const float *>(a.table);
-    const int64_t brow = (int64_t)b * a.bias_sb + (int64_t)nc * a.bias_sn;
-    const char *qb = static_cast<const char *>(a.q) + (int64_t)b * a.q_sb * 2;
-    const char *kb_ = static_cast<const char *>(a.k) + (int64_t)b * a.k_sb * 2;
-    const char *vb = static_cast<const char *>(a.v) + (int64_t)b * a.v_sb * 2;
-    const int64_t qsh = a.q_sh * 2, ksh = a.k_sh * 2, vsh = a.v_sh * 2;
-
-    // ---- registers of one head, loaded one head ahead
-    uint4 qf[2], kf[KBW], vr[PCV];
-    uint2 qb4 = make_uint2(0, 0), bk4 = make_uint2(0, 0), bv4 = make_uint2(0, 0);
-    float bs[RJ];
-    auto load_head = [&](int h) {
-        const char *Qh = qb + h * qsh, *Kh = kb_ + h * ksh, *Vh = vb + h * vsh;
-#pragma unroll
-        for (int qh = 0; qh < 2; ++qh) qf[qh] = ld16(Qh + qoff[qh]);  // B operand: query rows, 8 channels
-        if (blank) {
-            qb4 = ld8(Qh + qboff);
-            bk4 = ld8(static_cast<const char *>(a.blank_k) + (h * HD + 4 * jl) * 2);
-            bv4 = ld8(static_cast<const char *>(a.blank_v) + (h * HD + 4 * jl) * 2);
-        }
-#pragma unroll
-        for (int i = 0; i < KBW; ++i)
-            if (w + 4 * i < nkb) kf[i] = ld16(Kh + koff[i]);  // A operand: union row, 8 channels
-#pragma unroll
-        for (int i = 0; i < PCV; ++i)
-            if (16 * w + 64 * i < Up) vr[i] = ld16(Vh + voff[i]);  // this wave's rows [16w + 64i, +16)
-        // raw values: the selects wait until use, so these loads stay in flight
-#pragma unroll
-        for (int r = 0; r < RJ; ++r) {
-            if constexpr (BIAS == 1) {
-                bs[r] = use[r] ? load_any(a.bias, a.bias_dtype, brow + (int64_t)h * a.bias_sh + jl + LPQ * r) : 0.f;
-            } else if constexpr (BIAS == 2 || BIAS == 4) {
-                bs[r] = tab[r] >= 0 ? table[tab[r] * H + h] : 0.f;
-            } else if constexpr (BIAS == 3) {
-                const float *pw = a.pos_w + h * 5;
-                bs[r] = use[r] ? cont_bias(pw, a.pos_b[h], fx[r], fy[r]) : 0.f;
-            } else {
-                bs[r] = 0.f;
-            }
-        }
-    };
-
-    load_head(0);
-    for (int h = 0; h < H; ++h) {
-        // V rows into LDS as they are (rows past U as zeros): one 16-byte store per piece
-#pragma unroll
-        for (int i = 0; i < PCV; ++i)
-            if (16 * w + 64 * i < Up) {
-                const int pc = t + THREADS * i, s = pc >> 2, dc = pc & 3;
-                *reinterpret_cast<uint4 *>(&Vs[s * VRP + dc * 8]) = s < U ? vr[i] : make_uint4(0, 0, 0, 0);
-            }
-        // S^T blocks (16 slots x 16 queries) -> S[query][slot]
-#pragma unroll
-        for (int i = 0; i < KBW; ++i)
-            if (w + 4 * i < nkb) {
-                const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int qh = 0; qh < 2; ++qh) {
-                    const f32x4 sv = MM::mma(kf[i], qf[qh], z);
-                    *reinterpret_cast<f32x4 *>(&sh.S[(16 * qh + rowq) * SP + (w + 4 * i) * 16 + 4 * grp]) = sv;
-                }
-            }
-        const uint2 qp = qb4, bkp = bk4, bvp = bv4;
-        float bcur[RJ];
-#pragma unroll
-        for (int r = 0; r < RJ; ++r) bcur[r] = bs[r];
-        // this head's K/V registers are consumed: the next head's loads now have the
-        // whole softmax, PV pass and store of this head to arrive
-        if (h + 1 < H) load_head(h + 1);
-        lds_barrier();
-
-        // ---- softmax in (query, neighbour) layout, log2 units
-        float s_[RJ];
-        float mloc = MASKED_LOGIT * LOG2E;
-#pragma unroll
-        for (int r = 0; r < RJ; ++r) {
-            const float v = *reinterpret_cast<const float *>(reinterpret_cast<const char *>(sh.S) + sadr[r]) * scale2 +
-                            bcur[r] * LOG2E;
-            s_[r] = use[r] ? v : -INFINITY;
-            mloc = fmaxf(mloc, s_[r]);
-        }
-        float sb = 0.f;
-        if (blank) {
-            float part = 0.f;
-            const uint32_t qw[2] = {qp.x, qp.y}, kw[2] = {bkp.x, bkp.y};
-#pragma unroll
-            for (int e = 0; e < 2; ++e)
-                part += MM::to_f32(uint16_t(qw[e] & 0xffffu)) * MM::to_f32(uint16_t(kw[e] & 0xffffu)) +
-                        MM::to_f32(uint16_t(qw[e] >> 16)) * MM::to_f32(uint16_t(kw[e] >> 16));
-            sb = grp8_sum(part) * scale2;
-            mloc = fmaxf(mloc, sb);
-        }
-        const float m = grp8_max(mloc);
-        // P row q overwrites S row q: clear the row's P span first (every union
-        // slot a query does not use must read 0).  The 8 lanes of a query are in
-        // one wave, whose LDS operations run in order, so the row's S reads above
-        // complete before these stores.  The S reads are fp32 and the P stores
-        // 16-bit / 128-bit: the compiler barrier keeps type-based alias analysis
-        // from moving the stores above the reads.
-        asm volatile("" ::: "memory");
-        {
-            uint4 *prow = reinterpret_cast<uint4 *>(Pb + q * PP);
-            for (int c = jl; c < Up / 8; c += LPQ) prow[c] = make_uint4(0, 0, 0, 0);
-        }
-        float lsum = 0.f;
-#pragma unroll
-        for (int r = 0; r < RJ; ++r) {
-            const float pr = __builtin_amdgcn_exp2f(s_[r] - m);
-            lsum += pr;
-            *reinterpret_cast<uint16_t *>(reinterpret_cast<char *>(Pb) + padr[r]) = MM::from_f32(pr);
-        }
-        const float pblank = blank ? __builtin_amdgcn_exp2f(sb - m) : 0.f;
-        const float l = grp8_sum(lsum) + pblank + (nmq > 0.f ? nmq * __builtin_amdgcn_exp2f(MASKED_LOGIT * LOG2E - m) : 0.f);
-        if (jl == 0) {
-            linfo[q][0] = __builtin_amdgcn_rcpf(l + 1e-12f);  // 1 ulp: outputs are 16-bit
-            linfo[q][1] = pblank;
-            if (a.lse && qlive) a.lse[((int64_t)b * H + h) * N + n] = m * 0.6931471805599453f + __logf(l + 1e-12f);
-        }
-        lds_barrier();
-
-        // ---- O = P V_u: wave w owns queries 16 (w & 1) .. +16, channels 16 (w >> 1) .. +16;
-        // the B operand (8 slots of channel 16 ch + rowq) comes from two transposing reads
-        {
-            const int qh = w & 1, ch = w >> 1;
-            f32x4 o = {0.f, 0.f, 0.f, 0.f};
-            const uint16_t *vcol = Vs + (8 * grp + trk) * VRP + 16 * ch + 4 * tra;
-            for (int kb2 = 0; kb2 < nkb2; ++kb2) {
-                const int col = kb2 * 32 + 8 * grp;
-                const uint4 pa = *reinterpret_cast<const uint4 *>(&Pb[(16 * qh + rowq) * PP + col]);
-                const uint2 va = lds_read_tr16(vcol + kb2 * 32 * VRP);
-                const uint2 vb2 = lds_read_tr16(vcol + (kb2 * 32 + 4) * VRP);
-                o = MM::mma(pa, make_uint4(va.x, va.y, vb2.x, vb2.y), o);
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) Ob[(16 * qh + 4 * grp + i) * OP + 16 * ch + rowq] = o[i];
-        }
-        lds_barrier();
-
-        // ---- normalise, blank value, store: query q, channels 4 jl .. +4
-        {
-            const int d0 = 4 * jl;
-            const float4 ov = *reinterpret_cast<const float4 *>(&Ob[q * OP + d0]);
-            const float pbv = linfo[q][1], inv = linfo[q][0];
-            float x[4] = {ov.x, ov.y, ov.z, ov.w};
-            if (blank) {
-                const uint32_t vw[2] = {bvp.x, bvp.y};
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    x[2 * e] += pbv * MM::to_f32(uint16_t(vw[e] & 0xffffu));
-                    x[2 * e + 1] += pbv * MM::to_f32(uint16_t(vw[e] >> 16));
-                }
-            }
-            uint2 packed;
-            packed.x = uint32_t(MM::from_f32(x[0] * inv)) | (uint32_t(MM::from_f32(x[1] * inv)) << 16);
-            packed.y = uint32_t(MM::from_f32(x[2] * inv)) | (uint32_t(MM::from_f32(x[3] * inv)) << 16);
-            if (qlive)
-                *reinterpret_cast<uint2 *>(static_cast<T *>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh +
-                                           (int64_t)n * a.o_sn + d0) = packed;
-        }
-        // The next head's first LDS writes (V, S) touch regions whose last readers
-        // (PV, softmax) finished before the barrier above; its Ob / linfo writes come
-        // after its own first barrier, which every lane reaches only after this store.
-    }
-}
-
-// The tiles the MFMA kernel flagged: their TQ x H rows through the per-row routine.
-template <typename T, int BIAS>
-__global__ __launch_bounds__(THREADS) void nbhd_attn_tile_fallback_kernel(const aff_nbhd_attn_args a, int ntiles) {
-    using namespace tile;
-    const uint8_t *flags = static_cast<const uint8_t *>(a.ws);
-    const int tiles = (a.N + TQ - 1) / TQ;
-    const int sub = threadIdx.x & 3, rr = threadIdx.x >> 2;
-    for (int tl = blockIdx.x; tl < ntiles; tl += gridDim.x) {
-        if (!flags[tl]) continue;
-        const int b = tl / tiles, n0 = (tl % tiles) * TQ;
-        for (int p = rr; p < TQ * a.H; p += THREADS / 4) {
-            const int qq = p % TQ, h = p / TQ;
-            if (n0 + qq < a.N) attend_row<T, HD, BIAS, 8>(a, b, h, n0 + qq, sub);
-        }
-    }
-}
-
-// ------------------------------------------------------------------------
-// Wave-per-head tile kernel (16-bit q/k/v, head_dim 32, M <= 64, bias modes
-// 0, 2 and 4).
-//
-// One workgroup takes 32 consecutive queries of one image.  Set-up (all four
-// waves) builds the union of the tile's neighbour rows as the tile kernel
-// above does, and a dense [query][union slot] table `pw` of 16-bit codes:
-// 0 = the slot is not one of the query's neighbours, 1 = neighbour with a
-// zero bias, e >= 2 = neighbour whose bias is entry e of the bias window `tw`.
-// The window holds the rows of the [T*T, H] bias table that the tile's
-// (query, neighbour) offsets select - a few hundred entries for spatially
-// coherent tokens - so every bias read is an LDS read; a tile whose offsets
-// span more than the window reads the table in global memory instead
-// (e = 2 + table row).  tw entry 0 is -inf and entry 1 is 0 for every head.
-//
-// Then each wave owns one head at a time and runs without workgroup
-// barriers.  Per 32-slot chunk of the union:
-//   S^T (32 slots x 32 queries) = K_chunk Q^T       2 x v_mfma_f32_32x32x16
-//   logits (log2 units) = S * scale * log2(e) + bias(pw) * log2(e)
-//   online softmax per query: lane l and lane l ^ 32 hold the 16 + 16 slots
-//   of query l & 31, so the chunk maximum is one permlane32 swap
-//   O^T (32 channels x 32 queries) += V_chunk^T P^T    2 x v_mfma_f32_32x32x16
-// P^T is the S result itself converted to 16 bits: the PV contraction takes
-// its k index in the order the S result lays slots out in the lanes, and
-// V^T is read in that same order from the chunk's V rows in LDS by
-// ds_read_b64_tr_b16.  K and V rows are fetched one chunk ahead.
-// Tiles this kernel cannot take (union wider than 224 rows, index window
-// wider than 8192, an index repeated within one query, a per-head mask) run
-// the per-row routine in the same workgroup.
-// ------------------------------------------------------------------------
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 template <typename T> struct Mfma32;
@@ -800,300 +284,49 @@ __device__ __forceinline__ float pair_sum(float v) {
 // per row (head_dim 32), 4 neighbours per block so that its registers stay
 // below the wave kernel's own.
 template <typename T, int BIAS>
-__device__ __forceinline__ void tile_rows(const aff_nbhd_attn_args &a, int b, int n0, int nq) {
+__device__ __forceinline__ void tile_rows(const aff_nbhd_attn_args &a, int b, int n0, int nq, int hb, int hn) {
     const int sub = threadIdx.x & 3, rr = threadIdx.x >> 2;
-    for (int p = rr; p < nq * a.H; p += THREADS / 4) {
-        const int qq = p % nq, hd = p / nq;
+    for (int p = rr; p < nq * hn; p += THREADS / 4) {
+        const int qq = p % nq, hd = hb + p / nq;
         if (n0 + qq < a.N) attend_row<T, 32, BIAS, 4>(a, b, hd, n0 + qq, sub);
     }
 }
 
-template <typename T, int BIAS, bool IDX64, bool BLANK>
-__global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nbhd_attn_args a) {
+// Head phase of one wave over a 32-query tile whose union (U rows, ulist), codes (pw)
+// and bias store (bm) are in LDS: heads h0, h0 + hstep, ... below hend.  The bias of
+// head h for a (query, neighbour) code sits at byte 4 * (h - hbase) + code of bm.
+// nm: masked (live) neighbours of this lane's query; vbuf: the wave's V chunk buffer.
+//
+// Per 32-slot chunk:
+//   S^T (32 slots x 32 queries) = K_chunk Q^T       2 x v_mfma_f32_32x32x16
+//   logits (log2 units) = S * scale * log2(e) + bias(pw) * log2(e)
+//   online softmax per query: lane l and lane l ^ 32 hold the 16 + 16 slots
+//   of query l & 31, so the chunk maximum is one permlane32 swap
+//   O^T (32 channels x 32 queries) += V_chunk^T P^T    2 x v_mfma_f32_32x32x16
+// P^T is the S result itself converted to 16 bits: the PV contraction takes
+// its k index in the order the S result lays slots out in the lanes, and
+// V^T is read in that same order from the chunk's V rows in LDS by
+// ds_read_b64_tr_b16.  K and V rows are fetched one chunk ahead.
+template <typename T, bool BLANK>
+__device__ __forceinline__ void wave_head_one(const aff_nbhd_attn_args &a, int b, int n0, int U, const int *ulist,
+                                              const uint16_t *pw, const float *bm, float nm, uint16_t *vbuf, int h,
+                                              int hbase) {
     using namespace wt;
     using MM = Mfma32<T>;
-    // pw[q][slot]: byte offset in bm of the (query, neighbour) pair's biases; 0 (the
-    // -inf entry) where the union slot is not one of the query's neighbours
-    __shared__ __align__(16) uint16_t pw[TQ * PWP];
-    // bm: biases times log2(e): [H] -inf, [H] zero, then [TQ][M][H]
-    __shared__ __align__(16) float bm[BMW];
-    __shared__ int ulist[UMAX];
-    struct SetupLds {
-        uint8_t flg[WWORDS * 32];  // one byte per index of the window: a neighbour row
-        uint32_t bits[WWORDS];     // the same flags packed 32 to a word
-        uint32_t pref[WWORDS];     // union slots before each word
-    };
-    __shared__ __align__(16) union {
-        SetupLds s;
-        uint16_t vb[NW][32 * VRP];  // per-wave V chunk (head phase)
-    } sh;
-    __shared__ float nmq_s[TQ];
-    __shared__ int red[4];  // 0 flagged, 1 repeated index, 2 U
-
-    const int t = threadIdx.x, lane = t & 63;
-    const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: heads index scalar buffers
-    const int q = t >> 3, jl = t & 7;
-    const int N = a.N, M = a.M, H = a.H;
-    const int tiles = (N + TQ - 1) / TQ;
-    const int tile = int(xcd_swizzle(blockIdx.x, gridDim.x));
-    const int b = tile / tiles;
-    const int n0 = (tile % tiles) * TQ;
-    const int n = n0 + q;
-    const bool qlive = n < N;
-    const int nc = min(n, N - 1);
-    const int nr = (M + LPQ - 1) / LPQ;  // entries per set-up lane that exist (uniform)
-
-    if (t < 4) red[t] = 0;
-    for (int i = t; i < WWORDS * 2; i += THREADS) reinterpret_cast<uint4 *>(sh.s.flg)[i] = make_uint4(0, 0, 0, 0);
-    for (int i = t; i < TQ * PWP / 8; i += THREADS) reinterpret_cast<uint4 *>(pw)[i] = make_uint4(0, 0, 0, 0);
-    if (t < H) {
-        bm[t] = -INFINITY;
-        bm[H + t] = 0.f;
-    }
-
-    // ---- this lane's (query, neighbour) entries j = jl + 8 r.  Loads are unconditional
-    // buffer loads at 32-bit offsets inside this image's planes (clamped to entry M - 1
-    // and row nc; the host keeps the offsets below 2^31), validity is a select.
+    const int lane = threadIdx.x & 63;
+    const int N = a.N, H = a.H;
     auto rsrc = [](const void *p) {
         return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, -1, 0x00020000);
     };
-    const int mlast = max(M - 1, 0);
-    const auto r_mi = rsrc(static_cast<const char *>(a.member_idx) + (int64_t)b * a.mi_sb * (IDX64 ? 8 : 4));
-    const uint32_t mi_off = uint32_t(nc) * uint32_t(a.mi_sn);
-    int idx[RJ];
-    bool use[RJ];
-    int nmask = 0;
-#pragma unroll
-    for (int r = 0; r < RJ; ++r) {
-        use[r] = false;
-        idx[r] = nc;
-        if (r >= nr) continue;
-        const int j = jl + LPQ * r, jc = min(j, mlast);
-        const bool live = qlive && j < M;
-        bool ok;
-        int ix;
-        if constexpr (IDX64) {
-            const auto v2 = __builtin_amdgcn_raw_buffer_load_b64(r_mi, int((mi_off + jc) * 8), 0, 0);
-            const int64_t v = int64_t(uint64_t(v2[0]) | (uint64_t(v2[1]) << 32));
-            ok = live && v >= 0 && v < N;
-            ix = int(v);
-        } else {
-            const int v = int(__builtin_amdgcn_raw_buffer_load_b32(r_mi, int((mi_off + jc) * 4), 0, 0));
-            ok = live && unsigned(v) < unsigned(N);
-            ix = v;
-        }
-        if (a.mask) {
-            const auto r_mk = rsrc(a.mask + (int64_t)b * a.mask_sb);
-            ok = ok && __builtin_amdgcn_raw_buffer_load_b8(r_mk, int(uint32_t(nc) * uint32_t(a.mask_sn) + jc), 0, 0) != 0;
-        }
-        use[r] = ok;
-        idx[r] = ok ? ix : nc;
-        nmask += (live && !ok) ? 1 : 0;
-    }
-
-    // ---- biases of the entries, every head, times log2(e), for bm.  Table modes
-    // (2, 4): the entries' table-row inputs (pe rows, or the neighbours' coordinates)
-    // are loaded here and stay in flight through the union steps; the rows are read
-    // and bm written after the slots (write_table_biases).  Modes 1 and 3 store at
-    // once; mode 0 stores zeros.
-    const int rowq_b = 2 * H + q * M * H;  // bm word of (q, j = 0, h = 0)
-    const bool fast4 = (BIAS == 2 || BIAS == 4) && H == 4 && a.table_dtype == AFF_F32;
-    float2 gq[RJ];   // BIAS 4: neighbour coordinates
-    int64_t prow[RJ];  // BIAS 2: pe rows
-    float pqx = 0.f, pqy = 0.f;
-    const float *pos_b = nullptr;
-    if constexpr (BIAS == 3 || BIAS == 4) {
-        pos_b = a.pos + (int64_t)b * a.pos_sb;
-        const float2 pq = *reinterpret_cast<const float2 *>(pos_b + (int64_t)nc * a.pos_sn);
-        pqx = pq.x;
-        pqy = pq.y;
-    }
-    const int Tw = 2 * a.rel_width + 1;
-#pragma unroll
-    for (int r = 0; r < RJ; ++r) {
-        gq[r] = make_float2(0.f, 0.f);
-        prow[r] = -1;
-        if (r >= nr) continue;
-        const int j = jl + LPQ * r;
-        if constexpr (BIAS == 4) {
-            gq[r] = *reinterpret_cast<const float2 *>(pos_b + (int64_t)idx[r] * a.pos_sn);  // idx[r] is a valid row
-        } else if constexpr (BIAS == 2) {
-            if (use[r]) {
-                const int64_t e = (int64_t)b * a.pe_sb + (int64_t)nc * a.pe_sn + j;
-                prow[r] = a.pe_is_i64 ? static_cast<const int64_t *>(a.pe_idx)[e]
-                                      : int64_t(static_cast<const int32_t *>(a.pe_idx)[e]);
-            }
-        } else if constexpr (BIAS == 1) {
-            if (use[r]) {
-                float *dst = bm + rowq_b + j * H;
-                const int64_t e = (int64_t)b * a.bias_sb + (int64_t)nc * a.bias_sn + j;
-                for (int h = 0; h < H; ++h) dst[h] = load_any(a.bias, a.bias_dtype, e + (int64_t)h * a.bias_sh) * LOG2E;
-            }
-        } else if constexpr (BIAS == 3) {
-            if (use[r]) {
-                float *dst = bm + rowq_b + j * H;
-                const float2 g = *reinterpret_cast<const float2 *>(pos_b + (int64_t)idx[r] * a.pos_sn);
-                for (int h = 0; h < H; ++h) dst[h] = cont_bias(a.pos_w + h * 5, a.pos_b[h], g.x - pqx, g.y - pqy) * LOG2E;
-            }
-        } else {
-            // no bias: zero entries, so that every (query, neighbour) pair still has its own code
-            if (use[r])
-                for (int h = 0; h < H; ++h) bm[rowq_b + j * H + h] = 0.f;
-        }
-    }
-    auto table_row = [&](int r) -> int64_t {
-        if constexpr (BIAS == 2) return prow[r];
-        else return pe_from_coords32(pqx, pqy, gq[r].x, gq[r].y, float(a.rel_width), float(Tw));
-    };
-    // fp32 table, 4 heads: one 16-byte row per entry, loaded after the bits step and
-    // stored to bm after the slots step
-    float4 tv[RJ];
-    float tsc[RJ];
-    auto load_table_rows = [&]() {
-        if constexpr (BIAS == 2 || BIAS == 4) {
-            if (fast4) {
-#pragma unroll
-                for (int r = 0; r < RJ; ++r) {
-                    tv[r] = make_float4(0.f, 0.f, 0.f, 0.f);
-                    tsc[r] = 0.f;
-                    if (r >= nr || !use[r]) continue;
-                    const int64_t row = table_row(r);
-                    const bool in = row >= 0 && row < a.table_rows;
-                    tsc[r] = in ? LOG2E : 0.f;
-                    tv[r] = reinterpret_cast<const float4 *>(a.table)[in ? row : 0];
-                }
-            }
-        }
-    };
-    auto write_table_biases = [&]() {
-        if constexpr (BIAS == 2 || BIAS == 4) {
-#pragma unroll
-            for (int r = 0; r < RJ; ++r) {
-                if (r >= nr || !use[r]) continue;
-                float *dst = bm + rowq_b + (jl + LPQ * r) * H;
-                if (fast4) {
-                    const float sc = tsc[r];
-                    *reinterpret_cast<float4 *>(dst) = make_float4(tv[r].x * sc, tv[r].y * sc, tv[r].z * sc, tv[r].w * sc);
-                } else {
-                    const int64_t row = table_row(r);
-                    const bool in = row >= 0 && row < a.table_rows;
-                    for (int h = 0; h < H; ++h) dst[h] = in ? load_any(a.table, a.table_dtype, row * H + h) * LOG2E : 0.f;
-                }
-            }
-        }
-    };
-    // the cleared flags are visible before any wave sets one (the loads above stay
-    // in flight across this barrier)
-    lds_barrier();
-
-    // ---- union: a flag byte per neighbour row of the index window [wlo, wlo + 8192)
-    // (plain stores: every writer of a byte writes the same 1)
-    const int wlo = max(0, min(n0 + TQ / 2 - WWORDS * 16, N - WWORDS * 32));
-    bool outside = false;
-#pragma unroll
-    for (int r = 0; r < RJ; ++r) {
-        if (r >= nr) continue;
-        const unsigned o = unsigned(idx[r] - wlo);
-        const bool in = o < unsigned(WWORDS * 32);
-        outside = outside || (use[r] && !in);
-        if (use[r] && in) sh.s.flg[o] = 1;
-    }
-    if (outside) red[0] = 1;
-    {
-        const float nm = grp8_sum(float(nmask));
-        if (jl == 0) nmq_s[q] = nm;
-    }
-    lds_barrier();
-
-    // ---- flags -> bits (thread t packs window word t)
-    {
-        const uint4 f0 = reinterpret_cast<const uint4 *>(sh.s.flg)[2 * t];
-        const uint4 f1 = reinterpret_cast<const uint4 *>(sh.s.flg)[2 * t + 1];
-        const uint32_t d[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
-        uint32_t wbits = 0;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) wbits |= (((d[k] * 0x01020408u) >> 24) & 0xFu) << (4 * k);  // 4 flag bytes -> 4 bits
-        sh.s.bits[t] = wbits;
-    }
-    load_table_rows();
-    lds_barrier();
-
-    const bool flagged = (a.mask && a.mask_sh != 0) || red[0] != 0;
-    if (!flagged && w == 0) {
-        uint32_t c[4];
-        int tot = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            c[i] = __popc(sh.s.bits[lane * 4 + i]);
-            tot += c[i];
-        }
-        int inc = tot;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int v = __shfl_up(inc, o, 64);
-            if (lane >= o) inc += v;
-        }
-        int ex = inc - tot;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            sh.s.pref[lane * 4 + i] = ex;
-            ex += c[i];
-        }
-        if (lane == 63) red[2] = inc;
-    }
-    lds_barrier();
-    const int U = red[2];
-    bool fallback = flagged || U > UMAX;
-
-    // ---- union slots; pw codes (plain stores: a code is unique to its (query, neighbour)
-    // entry, so a repeated index within one query shows up as an overwritten code)
-    int slot[RJ];
-    if (!fallback) {
-        const int rowq = q * PWP;
-#pragma unroll
-        for (int r = 0; r < RJ; ++r) {
-            slot[r] = 0;
-            if (r >= nr) continue;
-            const int o = min(max(idx[r] - wlo, 0), WWORDS * 32 - 1), wd = o >> 5, bt = o & 31;
-            const int s_ = int(sh.s.pref[wd] + __popc(sh.s.bits[wd] & ((1u << bt) - 1u)));
-            slot[r] = s_;
-            if (use[r]) {
-                ulist[s_] = idx[r];
-                pw[rowq + s_] = uint16_t(uint32_t(rowq_b + (jl + LPQ * r) * H) * 4);
-            }
-        }
-        write_table_biases();
-    }
-    lds_barrier();
-    if (!fallback) {
-        bool dup = false;
-        const int rowq = q * PWP;
-#pragma unroll
-        for (int r = 0; r < RJ; ++r)
-            if (r < nr && use[r])
-                dup = dup || pw[rowq + slot[r]] != uint16_t(uint32_t(rowq_b + (jl + LPQ * r) * H) * 4);
-        if (__builtin_amdgcn_ballot_w64(dup) != 0 && lane == 0) red[1] = 1;
-        lds_barrier();
-        fallback = red[1] != 0;
-    }
-
-    if (fallback) {
-        tile_rows<T, BIAS>(a, b, n0, TQ);
-        return;
-    }
-
-    // ---- head phase: wave w, heads w, w + NW, ...
     const int hh = lane >> 5, ql = lane & 31;
     const int nch = (U + 31) >> 5;
     const bool qout = n0 + ql < N;
     const int qrow = min(n0 + ql, N - 1);
-    const float nm = nmq_s[ql];
     const uint32_t ksn2 = uint32_t(a.k_sn * 2), vsn2 = uint32_t(a.v_sn * 2);  // < 2^24, host-checked
     const uint32_t qoff = uint32_t(qrow) * uint32_t(a.q_sn * 2) + 32 * hh;
     const float scale2 = a.scale * LOG2E;
     // transposing-read role: 16-lane group g reads channels 16 (g & 1) + (lane & 15)
     const int kk = (lane & 15) >> 2, aa = lane & 3, cg = 16 * ((lane >> 4) & 1);
-    uint16_t *vbuf = sh.vb[w];
     const uint16_t *pwrow = pw + ql * PWP + 4 * hh;
     const uint32_t vst0 = (lane >> 2) * VRP + (lane & 3) * 8, vst1 = vst0 + 16 * VRP;
     const uint16_t *vtr = vbuf + (4 * hh + kk) * VRP + cg + 4 * aa;
@@ -1110,7 +343,7 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
         return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, int(off), 0, 0));
     };
 
-    for (int h = w; h < H; h += NW) {
+    {
         const auto rq = rsrc(static_cast<const char *>(a.q) + ((int64_t)b * a.q_sb + (int64_t)h * a.q_sh) * 2);
         const auto rk = rsrc(static_cast<const char *>(a.k) + ((int64_t)b * a.k_sb + (int64_t)h * a.k_sh) * 2);
         const auto rv = rsrc(static_cast<const char *>(a.v) + ((int64_t)b * a.v_sb + (int64_t)h * a.v_sh) * 2);
@@ -1141,7 +374,7 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
             sb = pair_sum(part) * scale2;
             m = fmaxf(m, sb);
         }
-        const char *bmh = reinterpret_cast<const char *>(bm) + 4 * h;
+        const char *bmh = reinterpret_cast<const char *>(bm) + 4 * (h - hbase);
         float lp = 0.f;
         f32x16 O;
 #pragma unroll
@@ -1263,6 +496,299 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
     }
 }
 
+// Heads h0, h0 + hstep, ... below hend, one after another (wave_head_one).
+template <typename T, bool BLANK>
+__device__ __forceinline__ void wave_heads(const aff_nbhd_attn_args &a, int b, int n0, int U, const int *ulist,
+                                           const uint16_t *pw, const float *bm, float nm, uint16_t *vbuf, int h0,
+                                           int hstep, int hend, int hbase) {
+    for (int h = h0; h < hend; h += hstep) wave_head_one<T, BLANK>(a, b, n0, U, ulist, pw, bm, nm, vbuf, h, hbase);
+}
+
+template <typename T, int BIAS, bool IDX64, bool BLANK>
+__global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nbhd_attn_args a, int HG) {
+    using namespace wt;
+    using MM = Mfma32<T>;
+    // pw[q][slot]: byte offset in bm of the (query, neighbour) pair's biases; 0 (the
+    // -inf entry) where the union slot is not one of the query's neighbours
+    __shared__ __align__(16) uint16_t pw[TQ * PWP];
+    // bm: biases of this workgroup's head group, times log2(e): [HG] -inf, [HG] zero,
+    // then [TQ][M][HG]
+    __shared__ __align__(16) float bm[BMW];
+    __shared__ int ulist[UMAX];
+    struct SetupLds {
+        uint8_t flg[WWORDS * 32];  // one byte per index of the window: a neighbour row
+        uint32_t bits[WWORDS];     // the same flags packed 32 to a word
+        uint32_t pref[WWORDS];     // union slots before each word
+    };
+    __shared__ __align__(16) union {
+        SetupLds s;
+        uint16_t vb[NW][32 * VRP];  // per-wave V chunk (head phase)
+    } sh;
+    __shared__ float nmq_s[TQ];
+    __shared__ int red[4];  // 0 flagged, 1 repeated index, 2 U
+
+    const int t = threadIdx.x, lane = t & 63;
+    const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: heads index scalar buffers
+    const int q = t >> 3, jl = t & 7;
+    const int N = a.N, M = a.M, H = a.H;
+    const int tiles = (N + TQ - 1) / TQ;
+    // workgroup = (tile, head group): the groups of one tile are adjacent, so on one XCD
+    const int ngroups = (H + HG - 1) / HG;
+    const int wg = int(xcd_swizzle(blockIdx.x, gridDim.x));
+    const int tile = wg / ngroups, hb = (wg % ngroups) * HG, hn = min(HG, H - hb);
+    const int b = tile / tiles;
+    const int n0 = (tile % tiles) * TQ;
+    const int n = n0 + q;
+    const bool qlive = n < N;
+    const int nc = min(n, N - 1);
+    const int nr = (M + LPQ - 1) / LPQ;  // entries per set-up lane that exist (uniform)
+
+    if (t < 4) red[t] = 0;
+    for (int i = t; i < WWORDS * 2; i += THREADS) reinterpret_cast<uint4 *>(sh.s.flg)[i] = make_uint4(0, 0, 0, 0);
+    for (int i = t; i < TQ * PWP / 8; i += THREADS) reinterpret_cast<uint4 *>(pw)[i] = make_uint4(0, 0, 0, 0);
+    if (t < HG) {
+        bm[t] = -INFINITY;
+        bm[HG + t] = 0.f;
+    }
+
+    // ---- this lane's (query, neighbour) entries j = jl + 8 r.  Loads are unconditional
+    // buffer loads at 32-bit offsets inside this image's planes (clamped to entry M - 1
+    // and row nc; the host keeps the offsets below 2^31), validity is a select.
+    auto rsrc = [](const void *p) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, -1, 0x00020000);
+    };
+    const int mlast = max(M - 1, 0);
+    const auto r_mi = rsrc(static_cast<const char *>(a.member_idx) + (int64_t)b * a.mi_sb * (IDX64 ? 8 : 4));
+    const uint32_t mi_off = uint32_t(nc) * uint32_t(a.mi_sn);
+    int idx[RJ];
+    bool use[RJ];
+    int nmask = 0;
+#pragma unroll
+    for (int r = 0; r < RJ; ++r) {
+        use[r] = false;
+        idx[r] = nc;
+        if (r >= nr) continue;
+        const int j = jl + LPQ * r, jc = min(j, mlast);
+        const bool live = qlive && j < M;
+        bool ok;
+        int ix;
+        if constexpr (IDX64) {
+            const auto v2 = __builtin_amdgcn_raw_buffer_load_b64(r_mi, int((mi_off + jc) * 8), 0, 0);
+            const int64_t v = int64_t(uint64_t(v2[0]) | (uint64_t(v2[1]) << 32));
+            ok = live && v >= 0 && v < N;
+            ix = int(v);
+        } else {
+            const int v = int(__builtin_amdgcn_raw_buffer_load_b32(r_mi, int((mi_off + jc) * 4), 0, 0));
+            ok = live && unsigned(v) < unsigned(N);
+            ix = v;
+        }
+        if (a.mask) {
+            const auto r_mk = rsrc(a.mask + (int64_t)b * a.mask_sb);
+            ok = ok && __builtin_amdgcn_raw_buffer_load_b8(r_mk, int(uint32_t(nc) * uint32_t(a.mask_sn) + jc), 0, 0) != 0;
+        }
+        use[r] = ok;
+        idx[r] = ok ? ix : nc;
+        nmask += (live && !ok) ? 1 : 0;
+    }
+
+    // ---- biases of the entries, every head, times log2(e), for bm.  Table modes
+    // (2, 4): the entries' table-row inputs (pe rows, or the neighbours' coordinates)
+    // are loaded here and stay in flight through the union steps; the rows are read
+    // and bm written after the slots (write_table_biases).  Modes 1 and 3 store at
+    // once; mode 0 stores zeros.
+    const int rowq_b = 2 * HG + q * M * HG;  // bm word of (q, j = 0, group head 0)
+    const bool fast4 = (BIAS == 2 || BIAS == 4) && HG == 4 && H % 4 == 0 && a.table_dtype == AFF_F32;
+    float2 gq[RJ];   // BIAS 4: neighbour coordinates
+    int64_t prow[RJ];  // BIAS 2: pe rows
+    float pqx = 0.f, pqy = 0.f;
+    const float *pos_b = nullptr;
+    if constexpr (BIAS == 3 || BIAS == 4) {
+        pos_b = a.pos + (int64_t)b * a.pos_sb;
+        const float2 pq = *reinterpret_cast<const float2 *>(pos_b + (int64_t)nc * a.pos_sn);
+        pqx = pq.x;
+        pqy = pq.y;
+    }
+    const int Tw = 2 * a.rel_width + 1;
+#pragma unroll
+    for (int r = 0; r < RJ; ++r) {
+        gq[r] = make_float2(0.f, 0.f);
+        prow[r] = -1;
+        if (r >= nr) continue;
+        const int j = jl + LPQ * r;
+        if constexpr (BIAS == 4) {
+            gq[r] = *reinterpret_cast<const float2 *>(pos_b + (int64_t)idx[r] * a.pos_sn);  // idx[r] is a valid row
+        } else if constexpr (BIAS == 2) {
+            if (use[r]) {
+                const int64_t e = (int64_t)b * a.pe_sb + (int64_t)nc * a.pe_sn + j;
+                prow[r] = a.pe_is_i64 ? static_cast<const int64_t *>(a.pe_idx)[e]
+                                      : int64_t(static_cast<const int32_t *>(a.pe_idx)[e]);
+            }
+        } else if constexpr (BIAS == 1) {
+            if (use[r]) {
+                float *dst = bm + rowq_b + j * HG;
+                const int64_t e = (int64_t)b * a.bias_sb + (int64_t)nc * a.bias_sn + j;
+                for (int h = 0; h < hn; ++h)
+                    dst[h] = load_any(a.bias, a.bias_dtype, e + (int64_t)(hb + h) * a.bias_sh) * LOG2E;
+            }
+        } else if constexpr (BIAS == 3) {
+            if (use[r]) {
+                float *dst = bm + rowq_b + j * HG;
+                const float2 g = *reinterpret_cast<const float2 *>(pos_b + (int64_t)idx[r] * a.pos_sn);
+                for (int h = 0; h < hn; ++h)
+                    dst[h] = cont_bias(a.pos_w + (hb + h) * 5, a.pos_b[hb + h], g.x - pqx, g.y - pqy) * LOG2E;
+            }
+        } else {
+            // no bias: zero entries, so that every (query, neighbour) pair still has its own code
+            if (use[r])
+                for (int h = 0; h < hn; ++h) bm[rowq_b + j * HG + h] = 0.f;
+        }
+    }
+    auto table_row = [&](int r) -> int64_t {
+        if constexpr (BIAS == 2) return prow[r];
+        else return pe_from_coords32(pqx, pqy, gq[r].x, gq[r].y, float(a.rel_width), float(Tw));
+    };
+    // fp32 table, 4 heads: one 16-byte row per entry, loaded after the bits step and
+    // stored to bm after the slots step
+    float4 tv[RJ];
+    float tsc[RJ];
+    auto load_table_rows = [&]() {
+        if constexpr (BIAS == 2 || BIAS == 4) {
+            if (fast4) {
+#pragma unroll
+                for (int r = 0; r < RJ; ++r) {
+                    tv[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    tsc[r] = 0.f;
+                    if (r >= nr || !use[r]) continue;
+                    const int64_t row = table_row(r);
+                    const bool in = row >= 0 && row < a.table_rows;
+                    tsc[r] = in ? LOG2E : 0.f;
+                    tv[r] = reinterpret_cast<const float4 *>(a.table)[((in ? row : 0) * H + hb) >> 2];
+                }
+            }
+        }
+    };
+    auto write_table_biases = [&]() {
+        if constexpr (BIAS == 2 || BIAS == 4) {
+#pragma unroll
+            for (int r = 0; r < RJ; ++r) {
+                if (r >= nr || !use[r]) continue;
+                float *dst = bm + rowq_b + (jl + LPQ * r) * HG;
+                if (fast4) {
+                    const float sc = tsc[r];
+                    *reinterpret_cast<float4 *>(dst) = make_float4(tv[r].x * sc, tv[r].y * sc, tv[r].z * sc, tv[r].w * sc);
+                } else {
+                    const int64_t row = table_row(r);
+                    const bool in = row >= 0 && row < a.table_rows;
+                    for (int h = 0; h < hn; ++h)
+                        dst[h] = in ? load_any(a.table, a.table_dtype, row * H + hb + h) * LOG2E : 0.f;
+                }
+            }
+        }
+    };
+    // the cleared flags are visible before any wave sets one (the loads above stay
+    // in flight across this barrier)
+    lds_barrier();
+
+    // ---- union: a flag byte per neighbour row of the index window [wlo, wlo + 8192)
+    // (plain stores: every writer of a byte writes the same 1)
+    const int wlo = max(0, min(n0 + TQ / 2 - WWORDS * 16, N - WWORDS * 32));
+    bool outside = false;
+#pragma unroll
+    for (int r = 0; r < RJ; ++r) {
+        if (r >= nr) continue;
+        const unsigned o = unsigned(idx[r] - wlo);
+        const bool in = o < unsigned(WWORDS * 32);
+        outside = outside || (use[r] && !in);
+        if (use[r] && in) sh.s.flg[o] = 1;
+    }
+    if (outside) red[0] = 1;
+    {
+        const float nm = grp8_sum(float(nmask));
+        if (jl == 0) nmq_s[q] = nm;
+    }
+    lds_barrier();
+
+    // ---- flags -> bits (thread t packs window word t)
+    {
+        const uint4 f0 = reinterpret_cast<const uint4 *>(sh.s.flg)[2 * t];
+        const uint4 f1 = reinterpret_cast<const uint4 *>(sh.s.flg)[2 * t + 1];
+        const uint32_t d[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+        uint32_t wbits = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) wbits |= (((d[k] * 0x01020408u) >> 24) & 0xFu) << (4 * k);  // 4 flag bytes -> 4 bits
+        sh.s.bits[t] = wbits;
+    }
+    load_table_rows();
+    lds_barrier();
+
+    const bool flagged = (a.mask && a.mask_sh != 0) || red[0] != 0;
+    if (!flagged && w == 0) {
+        uint32_t c[4];
+        int tot = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            c[i] = __popc(sh.s.bits[lane * 4 + i]);
+            tot += c[i];
+        }
+        int inc = tot;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(inc, o, 64);
+            if (lane >= o) inc += v;
+        }
+        int ex = inc - tot;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sh.s.pref[lane * 4 + i] = ex;
+            ex += c[i];
+        }
+        if (lane == 63) red[2] = inc;
+    }
+    lds_barrier();
+    const int U = red[2];
+    bool fallback = flagged || U > UMAX;
+
+    // ---- union slots; pw codes (plain stores: a code is unique to its (query, neighbour)
+    // entry, so a repeated index within one query shows up as an overwritten code)
+    int slot[RJ];
+    if (!fallback) {
+        const int rowq = q * PWP;
+#pragma unroll
+        for (int r = 0; r < RJ; ++r) {
+            slot[r] = 0;
+            if (r >= nr) continue;
+            const int o = min(max(idx[r] - wlo, 0), WWORDS * 32 - 1), wd = o >> 5, bt = o & 31;
+            const int s_ = int(sh.s.pref[wd] + __popc(sh.s.bits[wd] & ((1u << bt) - 1u)));
+            slot[r] = s_;
+            if (use[r]) {
+                ulist[s_] = idx[r];
+                pw[rowq + s_] = uint16_t(uint32_t(rowq_b + (jl + LPQ * r) * HG) * 4);
+            }
+        }
+        write_table_biases();
+    }
+    lds_barrier();
+    if (!fallback) {
+        bool dup = false;
+        const int rowq = q * PWP;
+#pragma unroll
+        for (int r = 0; r < RJ; ++r)
+            if (r < nr && use[r])
+                dup = dup || pw[rowq + slot[r]] != uint16_t(uint32_t(rowq_b + (jl + LPQ * r) * HG) * 4);
+        if (__builtin_amdgcn_ballot_w64(dup) != 0 && lane == 0) red[1] = 1;
+        lds_barrier();
+        fallback = red[1] != 0;
+    }
+
+    if (fallback) {
+        tile_rows<T, BIAS>(a, b, n0, TQ, hb, hn);
+        return;
+    }
+
+    // ---- head phase: wave w, heads hb + w, hb + w + NW, ... of the group
+    wave_heads<T, BLANK>(a, b, n0, U, ulist, pw, bm, nmq_s[lane & 31], sh.vb[w], hb + w, NW, hb + hn, hb);
+}
+
 using KernelFn = void (*)(const aff_nbhd_attn_args);
 
 template <typename T, int D>
@@ -1288,58 +814,20 @@ KernelFn pick_d(int D, int mode) {
     }
 }
 
-using TileFn = void (*)(const aff_nbhd_attn_args, int);
-
-template <typename T>
-TileFn pick_tile(int mode) {
-    switch (mode) {
-        case 0: return nbhd_attn_tile_kernel<T, 0>;
-        case 1: return nbhd_attn_tile_kernel<T, 1>;
-        case 2: return nbhd_attn_tile_kernel<T, 2>;
-        case 3: return nbhd_attn_tile_kernel<T, 3>;
-        default: return nbhd_attn_tile_kernel<T, 4>;
-    }
-}
-
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-using FallbackFn = void (*)(const aff_nbhd_attn_args, int);
-
-template <typename T>
-FallbackFn pick_fallback(int mode) {
-    switch (mode) {
-        case 0: return nbhd_attn_tile_fallback_kernel<T, 0>;
-        case 1: return nbhd_attn_tile_fallback_kernel<T, 1>;
-        case 2: return nbhd_attn_tile_fallback_kernel<T, 2>;
-        case 3: return nbhd_attn_tile_fallback_kernel<T, 3>;
-        default: return nbhd_attn_tile_fallback_kernel<T, 4>;
-    }
-}
-
-// The MFMA tile path takes 16-bit q/k/v with head_dim 32, up to 64 neighbours,
-// an fp32 bias table (modes 2 and 4), and row byte offsets inside one (b, h)
-// plane that fit the kernel's 32-bit offsets.
-inline bool use_tile_path(const aff_nbhd_attn_args &a) {
-    if (a.dtype == AFF_F32 || a.D != tile::HD || a.M > tile::MAXM) return false;
-    if ((a.bias_mode == 2 || a.bias_mode == 4) && a.table_dtype != AFF_F32) return false;
-    // 32-bit byte offsets built with 24-bit multiplies: row index and row stride in bytes below 2^24
-    auto plane_ok = [&](int64_t sn) {
-        return sn >= 0 && sn * 2 < ((int64_t)1 << 24) && ((int64_t)(a.N - 1) * sn + a.D) * 2 < ((int64_t)1 << 32);
-    };
-    return a.N < (1 << 24) && plane_ok(a.q_sn) && plane_ok(a.k_sn) && plane_ok(a.v_sn);
-}
-
 inline int64_t tile_count(const aff_nbhd_attn_args &a) {
-    return (int64_t)a.B * ((a.N + tile::TQ - 1) / tile::TQ);
+    return (int64_t)a.B * ((a.N + wt::TQ - 1) / wt::TQ);
 }
 
-// The wave-per-head kernel: 16-bit q/k/v, head_dim 32, M <= 64, every bias mode,
-// at most MAXH heads and H * M <= MAXHM (its per-(query, neighbour) bias store of
-// TQ * H * M fp32 words is addressed by 16-bit byte offsets), 32-bit offsets inside
-// one image's q/k/v, index and mask planes.
+// The wave-per-head kernel: 16-bit q/k/v, head_dim 32, M <= 64, every bias mode and
+// head count, 32-bit offsets inside one image's q/k/v, index and mask planes.  One
+// workgroup per (tile, head group) of wave_heads_per_group() heads: the group's
+// per-(query, neighbour) bias store, TQ * M * HG fp32 words, stays within MAXHM
+// per query (its 16-bit byte offsets) and the extra workgroups fill the chip when
+// a stage has few tiles and many heads.
 inline bool use_wave_path(const aff_nbhd_attn_args &a) {
     if (a.dtype == AFF_F32 || a.D != wt::HD || a.M > wt::MAXM) return false;
-    if (a.H > wt::MAXH || (int64_t)a.H * a.M > wt::MAXHM) return false;
     // 32-bit byte offsets inside one (b, h) plane, built with 24-bit multiplies
     auto plane_ok = [&](int64_t sn) {
         return sn >= 0 && sn * 2 < ((int64_t)1 << 24) && ((int64_t)(a.N - 1) * sn + a.D) * 2 < ((int64_t)1 << 32);
@@ -1352,14 +840,23 @@ inline bool use_wave_path(const aff_nbhd_attn_args &a) {
     return true;
 }
 
+// Heads per workgroup of the wave kernel: at most MAXHM / M (the bias store) and MAXH.
+inline int wave_heads_per_group(const aff_nbhd_attn_args &a) {
+    int hg = a.M > 0 ? wt::MAXHM / a.M : wt::MAXH;
+    hg = hg < 1 ? 1 : (hg > wt::MAXH ? wt::MAXH : hg);
+    return a.H < hg ? a.H : hg;
+}
+
+using WaveFn = void (*)(const aff_nbhd_attn_args, int);
+
 template <typename T, int BIAS>
-KernelFn pick_wave3(bool i64, bool blank) {
+WaveFn pick_wave3(bool i64, bool blank) {
     if (i64) return blank ? nbhd_attn_wave_kernel<T, BIAS, true, true> : nbhd_attn_wave_kernel<T, BIAS, true, false>;
     return blank ? nbhd_attn_wave_kernel<T, BIAS, false, true> : nbhd_attn_wave_kernel<T, BIAS, false, false>;
 }
 
 template <typename T>
-KernelFn pick_wave(const aff_nbhd_attn_args &a) {
+WaveFn pick_wave(const aff_nbhd_attn_args &a) {
     const bool i64 = a.idx_is_i64 != 0, blank = a.blank_k != nullptr;
     switch (a.bias_mode) {
         case 0: return pick_wave3<T, 0>(i64, blank);
@@ -1377,15 +874,12 @@ using namespace aff;
 
 extern "C" int aff_nbhd_attn_path(const aff_nbhd_attn_args *args) {
     if (args == nullptr) return -1;
-    if (attn::use_wave_path(*args)) return AFF_ATTN_PATH_WAVE;
-    if (attn::use_tile_path(*args)) return AFF_ATTN_PATH_TILE;
-    return AFF_ATTN_PATH_ROW;
+    return attn::use_wave_path(*args) ? AFF_ATTN_PATH_WAVE : AFF_ATTN_PATH_ROW;
 }
 
 extern "C" size_t aff_nbhd_attn_workspace_bytes(const aff_nbhd_attn_args *args) {
-    if (args == nullptr || (int64_t)args->B * args->H * args->N == 0) return 0;
-    if (attn::use_wave_path(*args)) return 0;
-    return attn::use_tile_path(*args) ? (size_t)attn::tile_count(*args) : 0;
+    (void)args;
+    return 0;
 }
 
 extern "C" aff_status aff_nbhd_attn_fwd(const aff_nbhd_attn_args *args, aff_stream_t stream) {
@@ -1430,28 +924,13 @@ extern "C" aff_status aff_nbhd_attn_fwd(const aff_nbhd_attn_args *args, aff_stre
     if (attn::use_wave_path(a)) {
         const int64_t ntiles = attn::tile_count(a);
         AFF_CHECK_ARG(ntiles < (int64_t)1 << 31, "aff_nbhd_attn_fwd: problem too large");
-        const attn::KernelFn fn = a.dtype == AFF_BF16 ? attn::pick_wave<bf16_t>(a) : attn::pick_wave<f16_t>(a);
-        hipLaunchKernelGGL(fn, dim3((unsigned)ntiles), dim3(attn::THREADS), 0, hs, a);
+        const int hg = attn::wave_heads_per_group(a);
+        const int64_t blocks = ntiles * ((a.H + hg - 1) / hg);
+        AFF_CHECK_ARG(blocks < (int64_t)1 << 31, "aff_nbhd_attn_fwd: problem too large");
+        const attn::WaveFn fn = a.dtype == AFF_BF16 ? attn::pick_wave<bf16_t>(a) : attn::pick_wave<f16_t>(a);
+        hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(attn::THREADS), 0, hs, a, hg);
         return check_launch("aff_nbhd_attn_fwd (wave tiles)");
     }
-    if (attn::use_tile_path(a)) {
-        const int64_t ntiles = attn::tile_count(a);
-        AFF_CHECK_ARG(ntiles < (int64_t)1 << 31, "aff_nbhd_attn_fwd: problem too large");
-        if (a.ws == nullptr || a.ws_bytes < (size_t)ntiles)
-            return fail(AFF_ERR_WORKSPACE, "aff_nbhd_attn_fwd: workspace of %lld bytes needed (got %zu)",
-                        (long long)ntiles, a.ws ? a.ws_bytes : (size_t)0);
-        const bool bf = a.dtype == AFF_BF16;
-        hipLaunchKernelGGL(bf ? attn::pick_tile<bf16_t>(a.bias_mode) : attn::pick_tile<f16_t>(a.bias_mode),
-                           dim3((unsigned)ntiles), dim3(attn::THREADS), 0, hs, a, (int)ntiles);
-        aff_status st = check_launch("aff_nbhd_attn_fwd (tiles)");
-        if (st != AFF_OK) return st;
-        // flagged tiles: a grid-stride pass whose blocks skip unflagged tiles
-        const int fb = (int)(ntiles < 2048 ? ntiles : 2048);
-        hipLaunchKernelGGL(bf ? attn::pick_fallback<bf16_t>(a.bias_mode) : attn::pick_fallback<f16_t>(a.bias_mode),
-                           dim3(fb), dim3(attn::THREADS), 0, hs, a, (int)ntiles);
-        return check_launch("aff_nbhd_attn_fwd (flagged tiles)");
-    }
-
     attn::KernelFn fn = nullptr;
     if (a.dtype == AFF_F32) fn = attn::pick_d<float>(a.D, a.bias_mode);
     else if (a.dtype == AFF_BF16) fn = attn::pick_d<bf16_t>(a.D, a.bias_mode);

@@ -24,13 +24,13 @@ from .. import _lib
 from ..utils.pos_embed import REL_POS_WIDTH
 
 _SUPPORTED_D = (8, 16, 32, 64, 128)
-PATH_NAMES = {0: "row", 1: "tile", 2: "wave"}
+PATH_NAMES = {0: "row", 2: "wave"}
 _path_log = None
 
 
 @contextlib.contextmanager
 def record_paths():
-    """Collect, in a list, the kernel family ("wave", "tile" or "row") that each
+    """Collect, in a list, the kernel family ("wave" or "row") that each
     aff_nbhd_attn_fwd call inside the block runs (aff_nbhd_attn_path)."""
     global _path_log
     prev, _path_log = _path_log, []

@@ -145,14 +145,11 @@ typedef struct aff_nbhd_attn_args {
     const void *blank_v;
     void *out; int64_t o_sb, o_sh, o_sn;
     float *lse;
-    void *ws; size_t ws_bytes; /* workspace: aff_nbhd_attn_workspace_bytes(args) bytes */
+    void *ws; size_t ws_bytes; /* workspace: aff_nbhd_attn_workspace_bytes(args) bytes (0 today) */
 } aff_nbhd_attn_args;
 
-/* Workspace the call with these arguments needs (0 when none).  The
- * matrix-core paths take 16-bit q/k/v with D == 32 and M <= 64; with
- * H * M <= 192 they need none, otherwise (fp32 table in bias modes 2 and 4)
- * one byte per 32-query tile.  Its contents on entry do not matter; calls
- * that share it must not overlap. */
+/* Workspace the call with these arguments needs: 0 (the kernels keep every
+ * per-tile table in LDS); kept so callers can size args->ws generically. */
 size_t aff_nbhd_attn_workspace_bytes(const aff_nbhd_attn_args *args);
 aff_status aff_nbhd_attn_fwd(const aff_nbhd_attn_args *args, aff_stream_t stream);
 
@@ -160,10 +157,10 @@ aff_status aff_nbhd_attn_fwd(const aff_nbhd_attn_args *args, aff_stream_t stream
  * launch, no validation beyond the path predicates).  A diagnostic with no
  * counterpart in the reference: tests use it to show which path a case takes.
  *   AFF_ATTN_PATH_ROW   per-row kernel (any dtype / head_dim)
- *   AFF_ATTN_PATH_TILE  16-bit MFMA tile kernel plus its flagged-tile pass
- *   AFF_ATTN_PATH_WAVE  16-bit MFMA wave-per-head kernel
+ *   AFF_ATTN_PATH_WAVE  16-bit MFMA kernel: 32-query tiles, one wave per head,
+ *                       workgroups of up to 4 heads (head_dim 32, M <= 64)
  * Returns -1 for a NULL pointer. */
-enum { AFF_ATTN_PATH_ROW = 0, AFF_ATTN_PATH_TILE = 1, AFF_ATTN_PATH_WAVE = 2 };
+enum { AFF_ATTN_PATH_ROW = 0, AFF_ATTN_PATH_WAVE = 2 };
 int aff_nbhd_attn_path(const aff_nbhd_attn_args *args);
 
 /* ------------------------------------------------------------------------ *

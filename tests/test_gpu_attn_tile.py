@@ -1,17 +1,13 @@
-"""MFMA paths of aff_nbhd_attn_fwd (bf16 / fp16, head_dim 32, M <= 64).
+"""The MFMA path of aff_nbhd_attn_fwd (bf16 / fp16, head_dim 32, M <= 64).
 
-Two matrix-core kernels serve these calls; aff_nbhd_attn_path() names the one
-a call takes and every test asserts it:
-
-* the wave kernel (H * M <= 192): one workgroup per 32 consecutive queries,
-  one wave per head.  Its set-up deduplicates the tile's neighbour indices
-  into a union of at most 224 token rows; tiles it cannot take (a wider
-  union, an index window over 8192, an index repeated within one query, a
-  per-head mask) run the per-row routine inside the same workgroup.
-* the tile kernel (H * M > 192, e.g. the encoder's 8- and 16-head stages):
-  the same 32-query union, S through LDS and a per-head loop; tiles it
-  cannot take are flagged in the workspace and computed by the flagged-tile
-  pass (nbhd_attn_tile_fallback_kernel) launched right after it.
+The wave kernel serves these calls, and aff_nbhd_attn_path() confirms it for
+every test: one workgroup per (32 consecutive queries, group of up to
+min(4, 192 // M) heads), one wave per head.  Its set-up deduplicates the
+tile's neighbour indices into a union of at most 224 token rows; tiles it
+cannot take (a wider union, an index window over 8192, an index repeated
+within one query, a per-head mask) run the per-row routine for the group's
+heads inside the same workgroup.  The cases with H * M > 192 (the encoder's
+8- and 16-head stages) run several head groups per tile.
 
 Each case below is built so that one of those branches runs, and every
 result is checked against the fp64 oracle (oracle/oracle.c) at the
@@ -64,8 +60,14 @@ def _qkv(B, H, N, dtype, seed):
     return q, k, v, bk, bv
 
 
+def _path(bias_mode, H, M):
+    """The kernel family aff_nbhd_attn_fwd picks for 16-bit head_dim-32 inputs, M <= 64:
+    the wave kernel, in workgroups of min(H, 192 // M) heads."""
+    return "wave"
+
+
 def _run(oracle_mod, dev, q, k, v, idx, scale, dense_bias=None, mask=None, bk=None, bv=None, expect=None, **kw):
-    """Run the kernel and the oracle; `expect` ("wave" / "tile") is the path the call must take."""
+    """Run the kernel and the oracle; `expect` ("wave" / "row") is the path the call must take."""
     print(f"[tile] B,H,N={tuple(q.shape[:3])} M={idx.shape[-1]} {q.dtype} {sorted(kw)} expect={expect}", flush=True)
     g = lambda t: None if t is None else t.to(dev)
     with record_paths() as paths:
@@ -107,7 +109,7 @@ def test_tile_bias_modes(oracle_mod, dev, dtype, bias_mode):
         dense = oracle_mod.continuous_bias(pos.numpy(), idx.numpy(), w.numpy(), bb.numpy()).astype(np.float32)
         kw = dict(pos=pos.to(dev), pos_weight=w.to(dev), pos_bias=bb.to(dev))
     out, lse, ro, rl = _run(oracle_mod, dev, q, k, v, idx, 32 ** -0.5, dense_bias=dense, bk=bk, bv=bv,
-                            expect="wave", **kw)
+                            expect=_path(bias_mode, H, M), **kw)
     assert out.dtype == dtype
     _check(out, lse, ro, rl, bias_mode)
 
@@ -118,7 +120,7 @@ def test_tile_neighbour_counts(oracle_mod, dev, M):
     pos = _grid_coords(B, N, seed=20 + M)
     idx = knn(pos.to(dev), pos.to(dev), M).cpu() if M else torch.zeros((B, N, 0), dtype=torch.int64)
     q, k, v, bk, bv = _qkv(B, H, N, torch.bfloat16, seed=21)
-    _check(*_run(oracle_mod, dev, q, k, v, idx, 0.3, bk=bk, bv=bv, expect="wave"), f"M={M}")
+    _check(*_run(oracle_mod, dev, q, k, v, idx, 0.3, bk=bk, bv=bv, expect=_path("none", H, M)), f"M={M}")
 
 
 @pytest.mark.parametrize("blank", [False, True])
@@ -209,8 +211,8 @@ def test_tile_strided_interleaved_kv(oracle_mod, dev):
     _check(out_buf.permute(0, 2, 1, 3), None, ro, None, "strided")
 
 
-# ---------------------------------------------------------------- tile kernel --
-# H * M > 192: the wave kernel's bias store does not fit, the tile kernel runs.
+# ------------------------------------------------------------ head groups --
+# H * M > 192: several workgroups of up to 4 heads per tile.
 
 def _table(H, seed):
     """[T*T, H] bias table: a seeded Linear(5, H) over the offset features."""
@@ -236,15 +238,15 @@ def test_tile_kernel_many_heads(oracle_mod, dev, dtype, H, M, bias_mode):
     kw = dict(pe_idx=pe.to(dev), pe_table=table.to(dev)) if bias_mode == "table" else \
         dict(pos=pos.to(dev), pe_table=table.to(dev))
     out, lse, ro, rl = _run(oracle_mod, dev, q, k, v, idx, 32 ** -0.5, dense_bias=dense, bk=bk, bv=bv,
-                            expect="tile", **kw)
+                            expect=_path(bias_mode, H, M), **kw)
     assert out.dtype == dtype
     _check(out, lse, ro, rl, f"tile H={H} M={M} {bias_mode}")
 
 
 @pytest.mark.parametrize("case", ["repeat", "wide_union", "per_head_mask", "shared_mask"])
 def test_tile_kernel_flagged_tiles(oracle_mod, dev, case):
-    """Tiles the tile kernel flags (a repeated index, a union over 224 rows, a per-head mask)
-    run in the flagged-tile pass; a shared mask stays on the tile kernel."""
+    """Tiles the set-up rejects (a repeated index, a union over 224 rows, a per-head mask) run
+    the per-row routine for each head group; a shared mask stays on the matrix cores."""
     B, H, N, M = 1, 8, 640, 48
     pos = _grid_coords(B, N, seed=110).round()
     idx = knn(pos.to(dev), pos.to(dev), M).cpu()
@@ -265,7 +267,7 @@ def test_tile_kernel_flagged_tiles(oracle_mod, dev, case):
     pe = pe_index(pos, idx)
     dense = table[pe].permute(0, 3, 1, 2).contiguous().numpy()
     _check(*_run(oracle_mod, dev, q, k, v, idx, 0.3, dense_bias=dense, mask=mask, bk=bk, bv=bv,
-                 expect="tile", pe_idx=pe.to(dev), pe_table=table.to(dev)), f"flagged {case}")
+                 expect="wave", pe_idx=pe.to(dev), pe_table=table.to(dev)), f"flagged {case}")
 
 
 def test_tile_kernel_no_bias_no_blank(oracle_mod, dev):
@@ -273,4 +275,25 @@ def test_tile_kernel_no_bias_no_blank(oracle_mod, dev):
     pos = _grid_coords(B, N, seed=120)
     idx = knn(pos.to(dev), pos.to(dev), M).cpu()
     q, k, v, _, _ = _qkv(B, H, N, torch.float16, seed=121)
-    _check(*_run(oracle_mod, dev, q, k, v, idx, 0.3, expect="tile"), "tile no bias")
+    _check(*_run(oracle_mod, dev, q, k, v, idx, 0.3, expect="wave"), "tile no bias")
+
+
+@pytest.mark.parametrize("bias_mode", ["dense", "continuous"])
+def test_tile_kernel_dense_and_continuous(oracle_mod, dev, bias_mode):
+    """H * M > 192 with the dense and continuous bias forms: head groups of the wave kernel."""
+    B, H, N, M = 2, 8, 500, 48
+    pos = _grid_coords(B, N, seed=130)
+    idx = knn(pos.to(dev), pos.to(dev), M).cpu()
+    q, k, v, bk, bv = _qkv(B, H, N, torch.bfloat16, seed=131)
+    g = torch.Generator().manual_seed(132)
+    if bias_mode == "dense":
+        dense = (torch.randn((B, H, N, M), generator=g) * 0.5).bfloat16().float()
+        kw = dict(bias=dense.bfloat16().to(dev))
+        dense = dense.numpy()
+    else:
+        w = torch.rand((H, 5), generator=g) * 0.8 - 0.4
+        bb = torch.rand((H,), generator=g) * 0.2 - 0.1
+        dense = oracle_mod.continuous_bias(pos.numpy(), idx.numpy(), w.numpy(), bb.numpy()).astype(np.float32)
+        kw = dict(pos=pos.to(dev), pos_weight=w.to(dev), pos_bias=bb.to(dev))
+    _check(*_run(oracle_mod, dev, q, k, v, idx, 0.3, dense_bias=dense, bk=bk, bv=bv, expect="wave", **kw),
+           f"tile {bias_mode}")
