@@ -24,7 +24,7 @@ AFF_F32, AFF_F16, AFF_BF16 = 0, 1, 2
 KNN_NOALLOC_SCRATCH_BYTES = 16 << 20   # AFF_KNN_NOALLOC_SCRATCH_BYTES
 DTYPE_CODE = {torch.float32: AFF_F32, torch.float16: AFF_F16, torch.bfloat16: AFF_BF16}
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 P = ctypes.c_void_p
 I32 = ctypes.c_int
@@ -119,6 +119,8 @@ SIGNATURES = {
                                I32, I32, I32, I32, I32, I32, P, I64, I64, P]),
     "aff_cluster_members": (I32, [P, I32, I64, I64, P, I32, I64, I64, P, I64, I64, P, I64, I64,
                                   I32, I32, I32, I32, I32, I32, P, I32, P, P, I32, P]),
+    "aff_layer_norm_fwd": (I32, [P, I32, I64, P, I32, I64, P, P, I64, I32, F32, P]),
+    "aff_layer_norm_map_fwd": (I32, [P, I32, P, I32, P, P, P, I32, I32, I32, I32, I32, I32, I32, F32, P]),
 }
 
 _lib = None

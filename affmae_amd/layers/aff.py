@@ -21,6 +21,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from ..kernels.knn import knn
+from ..kernels.layer_norm import layer_norm_map, norm
 from ..kernels.nbhd_index import cluster_members
 from ..kernels.weighted_features import weighted_features
 from ..utils.geometry import space_filling_cluster
@@ -141,7 +142,7 @@ class ClusterMerging(nn.Module):
 
         if member_idx is None:
             feat_down = feat.gather(index=idx.expand(-1, -1, c), dim=1)
-            feat_down = self.global_linear(self.global_norm(feat_down))
+            feat_down = self.global_linear(norm(self.global_norm, feat_down, to_autocast=True))
             return pos_down, feat_down
 
         nbhd_size = member_idx.shape[-1]
@@ -155,8 +156,9 @@ class ClusterMerging(nn.Module):
 
         weights_table = self._weights_table(pe_idx.device, feat.dtype)
         inner_ch = weights_table.shape[-1]
-        weights = weights_table.gather(index=pe_idx.reshape(-1, 1).expand(-1, inner_ch), dim=0)
-        weights = weights.reshape(*pe_idx.shape, inner_ch)
+        # element gather of table rows (an index_select of 4-wide rows launches one block per row)
+        flat = pe_idx.unsqueeze(-1) * inner_ch + torch.arange(inner_ch, device=pe_idx.device)
+        weights = torch.take(weights_table, flat)
         if lp is not None:
             if cluster_mask is not None:
                 lp = lp * cluster_mask.unsqueeze(3)
@@ -165,7 +167,7 @@ class ClusterMerging(nn.Module):
             weights = weights * cluster_mask.unsqueeze(3)
 
         feat_down = weighted_features(weights, feat, member_idx.view(b, n_down, -1)).reshape(b, n_down, -1)
-        feat_down = self.norm(feat_down)
+        feat_down = norm(self.norm, feat_down, to_autocast=True)
         feat_down = self.linear(feat_down)
         return pos_down, feat_down
 
@@ -237,13 +239,13 @@ class ClusterTransformerBlock(nn.Module):
         """feat [b,n,c]; member_idx / cluster_mask / pe_idx [b,n,nbhd] -> [b,n,c]."""
         b, n, c = feat.shape
         assert c == self.dim, "dim does not accord to input"
-        a = self.attn(feat=self.norm1(feat), member_idx=member_idx, cluster_mask=cluster_mask, pe_idx=pe_idx,
-                      global_attn=global_attn)
+        a = self.attn(feat=norm(self.norm1, feat, to_autocast=True), member_idx=member_idx,
+                      cluster_mask=cluster_mask, pe_idx=pe_idx, global_attn=global_attn)
         if self.layer_scale:
             feat = feat + self.drop_path(self.gamma1 * a)
-            return feat + self.drop_path(self.gamma2 * self.mlp(self.norm2(feat)))
+            return feat + self.drop_path(self.gamma2 * self.mlp(norm(self.norm2, feat, to_autocast=True)))
         feat = feat + self.drop_path(a)
-        return feat + self.drop_path(self.mlp(self.norm2(feat)))
+        return feat + self.drop_path(self.mlp(norm(self.norm2, feat, to_autocast=True)))
 
     def extra_repr(self) -> str:
         return f"dim={self.dim}, num_heads={self.num_heads}, mlp_ratio={self.mlp_ratio}"
@@ -331,7 +333,7 @@ class BasicLayer(nn.Module):
                 return pos, feat, pos, feat
             feat_down = feat.gather(1, selection.unsqueeze(-1).expand(-1, -1, feat.shape[-1]))
             pos_down = pos.gather(1, selection.unsqueeze(-1).expand(-1, -1, pos.shape[-1]))
-            return pos, feat, pos_down, self.downsample_proj(self.downsample_norm(feat_down))
+            return pos, feat, pos_down, self.downsample_proj(norm(self.downsample_norm, feat_down, to_autocast=True))
         learned_prob = self.prob_net(feat).sigmoid()
         reserve_num = math.ceil(h / (stride * 2)) * math.ceil(w / (stride * 2))
         pos_down, feat_down = self.downsample(pos=pos, feat=feat, member_idx=member_idx,
@@ -385,6 +387,19 @@ class AFFPatchEmbed(nn.Module):
                 self.acts.append(nn.GELU())
             ch = out_ch
 
+    def _fused(self, x) -> bool:
+        """Inference on a GPU with LayerNorm2dImages + exact GELU between the
+        convolutions and a final LayerNorm: each mask / norm / GELU step runs as
+        one HIP kernel."""
+        if self.norm is None or not isinstance(self.norm, nn.LayerNorm) or not x.is_cuda:
+            return False
+        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
+            return False
+        if any(not isinstance(a, nn.GELU) or a.approximate != "none" for a in self.acts):
+            return False
+        chans = [ln.ln.normalized_shape[0] for ln in self.lns] + [self.norm.normalized_shape[0]]
+        return all(c <= 64 for c in chans) and all(isinstance(ln, LayerNorm2dImages) for ln in self.lns)
+
     def forward(self, x, ids_masked):
         ps = self.patch_size
         H, W = x.shape[-2:]
@@ -399,17 +414,33 @@ class AFFPatchEmbed(nn.Module):
             keep = torch.ones(B, th * tw, device=x.device, dtype=x.dtype)
             keep.scatter_(1, ids_masked, 0.0)
             keep = keep.view(B, 1, th, tw)
+        fused = self._fused(x)
         for i, proj in enumerate(self.projs):
             x = proj(x)
+            cell = max(ps >> (i + 1), 1)                       # map pixels per token side at this depth
+            last = i == len(self.projs) - 1
+            if fused:
+                # mask, LayerNorm (+ GELU) in one pass; the last one writes the tokens [b, h*w, c]
+                ln = self.norm if last else self.lns[i].ln
+                to_ac = torch.is_autocast_enabled("cuda") and not last
+                out_dtype = torch.get_autocast_dtype("cuda") if to_ac else (
+                    torch.float32 if torch.is_autocast_enabled("cuda") else x.dtype)
+                x = layer_norm_map(x, ln.weight, ln.bias, ln.eps, keep=keep, cell=cell, gelu=not last,
+                                   token_major=last, out_dtype=out_dtype)
+                continue
             if keep is not None:
-                cell = max(ps >> (i + 1), 1)                   # map pixels per token side at this depth
-                x = x * keep.repeat_interleave(cell, dim=2).repeat_interleave(cell, dim=3)
+                blocks = x.unflatten(3, (-1, cell)).unflatten(2, (-1, cell))   # b, c, th, cell, tw, cell
+                x = (blocks * keep[:, :, :, None, :, None]).flatten(4, 5).flatten(2, 3)
             if i < len(self.lns):
                 x = self.acts[i](self.lns[i](x))
-        b, c, h, w = x.shape
-        x = x.flatten(2).transpose(1, 2)
-        if self.norm is not None:
-            x = self.norm(x)
+        if fused:
+            h, w = th, tw
+            b = x.shape[0]
+        else:
+            b, c, h, w = x.shape
+            x = x.flatten(2).transpose(1, 2)
+            if self.norm is not None:
+                x = self.norm(x)
         ys, xs = torch.meshgrid(torch.arange(h, device=x.device), torch.arange(w, device=x.device), indexing='ij')
         pos = torch.stack([xs, ys], dim=2).reshape(1, h * w, 2).expand(b, -1, -1).to(x.dtype)
         return pos, x, h, w
@@ -477,7 +508,7 @@ class AFFEncoder(nn.Module):
         for i, layer in enumerate(self.layers):
             pos_out, x_out, pos, feat = layer(pos, feat, h=h, w=w, on_grid=False, stride=2 ** (i + 1))
             name = f"res{i + 2}"
-            out[name] = self.norms[i](x_out)
+            out[name] = norm(self.norms[i], x_out)
             out[f"{name}_pos"] = pos_out
             out[f"{name}_spatial_shape"] = (h, w)
         return out

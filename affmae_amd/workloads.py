@@ -161,8 +161,8 @@ def mae_encode(encoder, images, ids_keep, ids_masked, patch: int):
     th, tw = Hh // patch, Ww // patch
     keep = torch.ones((B, th * tw), device=images.device, dtype=images.dtype)
     keep.scatter_(1, ids_masked, 0.0)
-    keep_map = keep.view(B, 1, th, tw).repeat_interleave(patch, 2).repeat_interleave(patch, 3)
-    pos, feat, h, w = encoder.patch_embed(images * keep_map, ids_masked)
+    blocks = images.reshape(B, C, th, patch, tw, patch) * keep.view(B, 1, th, 1, tw, 1)
+    pos, feat, h, w = encoder.patch_embed(blocks.reshape(B, C, Hh, Ww), ids_masked)
     vis_feat = feat.gather(1, ids_keep.unsqueeze(-1).expand(-1, -1, feat.shape[-1]))
     vis_pos = pos.gather(1, ids_keep.unsqueeze(-1).expand(-1, -1, 2))
     return encoder(vis_feat, vis_pos, h, w)

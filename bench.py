@@ -317,6 +317,15 @@ def only_kernel(name: str, steps: int) -> int:
         fo = torch.empty((32, 2509, 128), dtype=torch.bfloat16, device=dev)
         po = torch.empty((32, 2509, 2), dtype=torch.float32, device=dev)
         fn = lambda: softmax_merge_launch(mp, sp, f, idx, 0.1, out=fo, out_pos=po)
+    elif name == "encoder":
+        from affmae_amd import workloads
+        enc = workloads.cfg5_encoder().to(dev).eval()
+        w5 = workloads.cfg5(B=8, img=1024, seed=0)
+        imgs, keep, masked = w5["images"].to(dev), w5["ids_keep"].to(dev), w5["ids_masked"].to(dev)
+
+        def fn():
+            with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+                return workloads.mae_encode(enc, imgs, keep, masked, 4)
     elif name == "deform":
         from affmae_amd.kernels.fused_deform_attn import ms_deformable_attention
         w4 = workloads.cfg4(B=32)
@@ -337,7 +346,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-oracle work (0 = skip)")
     ap.add_argument("--no-other", action="store_true", help="skip the config-3/4 kernel timings")
-    ap.add_argument("--only", choices=("attn", "knn", "merge", "deform", "copy"),
+    ap.add_argument("--only", choices=("attn", "knn", "merge", "deform", "encoder", "copy"),
                     help="launch only this kernel family --steps times (for rocprofv3 counter runs)")
     args = ap.parse_args()
 

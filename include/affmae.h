@@ -426,6 +426,40 @@ aff_status aff_cluster_members(const void *nearest, int near_is_i64, int64_t n_s
                                void *out_member, int out_is_i64, uint8_t *out_mask,
                                void *out_pe, int pe_is_i64, aff_stream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * aff_layer_norm_fwd — LayerNorm over the last dimension, forward.
+ * Replaces the encoder's nn.LayerNorm calls on token rows (reference
+ * src/layers/aff.py:96,108 block norms, :296 merge norm, :494 downsample
+ * norm, :726 stage norms).
+ *
+ * x [rows, C] (dtype x_dtype, row stride x_rs elements, unit channel stride)
+ * -> y [rows, C] (y_dtype, row stride y_rs): fp32 mean and biased variance,
+ * y = (x - mean) * rsqrt(var + eps) * weight + bias (weight / bias fp32 [C]
+ * or NULL, 16-byte aligned).  C % 8 == 0, C <= 4096, x / y and their row
+ * strides 16-byte aligned.  y_dtype may differ from x_dtype (an autocast consumer's dtype).
+ * ------------------------------------------------------------------------ */
+aff_status aff_layer_norm_fwd(const void *x, int x_dtype, int64_t x_rs, void *y, int y_dtype, int64_t y_rs,
+                              const float *weight, const float *bias, int64_t rows, int C, float eps,
+                              aff_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * aff_layer_norm_map_fwd — LayerNorm over the channels of a [B, C, H, W] map,
+ * with the masked patch embedding's mask and activation fused.
+ * Replaces LayerNorm2dImages + GELU after a masked convolution, and the
+ * final token LayerNorm of the patch embedding (reference
+ * src/layers/aff.py:514-526, 610-632).
+ *
+ * x [B, C, H, W] contiguous (x_dtype).  Per pixel: v = x * keep[b, token]
+ * when keep (fp32 [B, (H / cell) * (W / cell)], token = (y / cell) *
+ * (W / cell) + x / cell) is given, then LayerNorm over C (fp32 statistics,
+ * weight / bias fp32 [C] or NULL), then the exact-erf GELU when gelu != 0.
+ * Output y is [B, C, H, W] (token_major = 0) or [B, H * W, C]
+ * (token_major = 1), contiguous, y_dtype.  C <= 64.
+ * ------------------------------------------------------------------------ */
+aff_status aff_layer_norm_map_fwd(const void *x, int x_dtype, void *y, int y_dtype, const float *weight,
+                                  const float *bias, const float *keep, int cell, int B, int C, int H, int W,
+                                  int token_major, int gelu, float eps, aff_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
