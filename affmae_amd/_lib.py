@@ -24,7 +24,7 @@ AFF_F32, AFF_F16, AFF_BF16 = 0, 1, 2
 KNN_NOALLOC_SCRATCH_BYTES = 16 << 20   # AFF_KNN_NOALLOC_SCRATCH_BYTES
 DTYPE_CODE = {torch.float32: AFF_F32, torch.float16: AFF_F16, torch.bfloat16: AFF_BF16}
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 P = ctypes.c_void_p
 I32 = ctypes.c_int
@@ -90,6 +90,30 @@ class DeformArgs(ctypes.Structure):
     ]
 
 
+DEFORM_BWD_SHEPARD, DEFORM_BWD_IDW, DEFORM_BWD_SAMPLE, DEFORM_BWD_SAMPLE_SQ, DEFORM_BWD_GIVEN = 0, 1, 2, 3, 4
+
+
+class DeformBwdArgs(ctypes.Structure):
+    """Mirror of ``aff_deform_bwd_args`` (include/affmae.h)."""
+    _fields_ = [
+        ("mode", I32), ("B", I32), ("Q", I32), ("H", I32), ("S", I32), ("K", I32), ("C", I32), ("D", I32),
+        ("P", I32), ("Nkv", I32),
+        ("level_start", I32 * (DEFORM_MAX_LEVELS + 1)),
+        ("loc", P), ("loc_sb", I64), ("loc_sn", I64),
+        ("offsets", P), ("off_dtype", I32), ("off_sb", I64), ("off_sn", I64), ("off_sh", I64),
+        ("kv_pos", P), ("kp_sb", I64), ("kp_sn", I64),
+        ("idx", P), ("idx_is_i64", I32), ("i_sb", I64), ("i_sn", I64), ("i_sh", I64),
+        ("attn", P), ("attn_dtype", I32), ("at_sb", I64), ("at_sn", I64), ("at_sh", I64),
+        ("weights", P), ("w_dtype", I32), ("w_sb", I64), ("w_sn", I64), ("w_sh", I64),
+        ("dtype", I32),
+        ("values", P), ("v_sb", I64), ("v_sn", I64), ("v_sh", I64),
+        ("dout", P), ("do_sb", I64), ("do_sn", I64), ("do_sh", I64),
+        ("d_w_in", P), ("dwi_sb", I64), ("dwi_sn", I64), ("dwi_sh", I64),
+        ("power", P),
+        ("d_loc", P), ("d_attn", P), ("d_weights", P), ("d_kv_pos", P), ("d_values", P), ("d_power", P),
+    ]
+
+
 # Every symbol include/affmae.h declares, with (restype, argtypes).
 SIGNATURES = {
     "aff_last_error": (ctypes.c_char_p, []),
@@ -119,6 +143,8 @@ SIGNATURES = {
                                I32, I32, I32, I32, I32, I32, P, I64, I64, P]),
     "aff_cluster_members": (I32, [P, I32, I64, I64, P, I32, I64, I64, P, I64, I64, P, I64, I64,
                                   I32, I32, I32, I32, I32, I32, P, I32, P, P, I32, P]),
+    "aff_deform_bwd_workspace_bytes": (SZ, [ctypes.POINTER(DeformBwdArgs)]),
+    "aff_deform_bwd": (I32, [ctypes.POINTER(DeformBwdArgs), P, SZ, P]),
     "aff_layer_norm_fwd": (I32, [P, I32, I64, P, I32, I64, P, P, I64, I32, F32, P]),
     "aff_layer_norm_map_fwd": (I32, [P, I32, P, I32, P, P, P, I32, I32, I32, I32, I32, I32, I32, F32, P]),
 }

@@ -6,6 +6,8 @@ Drop-ins for src/layers/kernels/fused_deform_attn.py of the reference:
 launchers (:2387-2654) and ``fused_deformable_attention`` (:694, given
 neighbour indices).  ``ms_deformable_attention`` is the multi-level form:
 L levels x P points, K-NN per level with inverse-distance or Shepard weights.
+Every autograd Function has a backward through aff_deform_bwd (fixed-order
+sums, no float atomics).
 
 The sampling power is read on the device (no ``.item()`` host sync).
 """
@@ -127,6 +129,129 @@ def deform_launch(query_pos, kv_pos, level_start, offsets, attn, values, power, 
     return out
 
 
+def _inner_contig(t, dims):
+    """t with its last `dims` dimensions contiguous (a copy only when they are not)."""
+    exp = 1
+    for i in range(1, dims + 1):
+        if t.shape[-i] != 1 and t.stride(-i) != exp:
+            return t.contiguous()
+        exp *= t.shape[-i]
+    return t
+
+
+def deform_backward_launch(mode, dout, *, idx, loc=None, offsets=None, kv_pos=None, attn=None, weights=None,
+                           values=None, d_w_in=None, power=None, level_start=None, P=None, Nkv=None,
+                           want_loc=False, want_attn=False, want_weights=False, want_kv=False, want_values=False,
+                           want_power=False):
+    """aff_deform_bwd over rows (b, q, h) of S samples x K neighbours.
+
+    idx [B,Q,H,S,K]; loc [B,Q,D] fp32; offsets [B,Q,H,S,D]; kv_pos [B,Nkv,D];
+    attn [B,Q,H,S]; weights / d_w_in [B,Q,H,S,K]; values [B,Nkv,H,C] and
+    dout [B,Q,H,C] (or dout None with d_w_in).  level_start: row offsets of
+    the levels (level of sample s = s // P).  Returns a dict with the wanted
+    gradients: d_loc [B,Q,H,S,D], d_attn [B,Q,H,S], d_weights [B,Q,H,S,K],
+    d_kv_pos [B,Nkv,D] (fp32), d_values [B,Nkv,H,C] (values.dtype), d_power [1].
+    """
+    lib = _lib.load()
+    dev = _lib.require_cuda(idx, dout, loc, kv_pos, values, d_w_in)
+    B, Q, H, S, K = idx.shape
+    a = _lib.DeformBwdArgs()
+    a.mode, a.B, a.Q, a.H, a.S, a.K = mode, B, Q, H, S, K
+    D = loc.shape[-1] if loc is not None else (kv_pos.shape[-1] if kv_pos is not None else 0)
+    a.D = D
+    a.P = P or S
+    if Nkv is None:
+        Nkv = values.shape[1] if values is not None else kv_pos.shape[1]
+    a.Nkv = Nkv
+    ls = list(level_start) if level_start is not None else [0, Nkv]
+    for i, v in enumerate(ls):
+        a.level_start[i] = int(v)
+    keep = []
+    ix = idx if idx.dtype in (torch.int32, torch.int64) else idx.to(torch.int64)
+    ix = _inner_contig(ix, 2)
+    keep.append(ix)
+    a.idx, a.idx_is_i64 = ix.data_ptr(), 1 if ix.dtype == torch.int64 else 0
+    a.i_sb, a.i_sn, a.i_sh = ix.stride(0), ix.stride(1), ix.stride(2)
+    if loc is not None:
+        lc = _f32pos(loc)
+        keep.append(lc)
+        a.loc, a.loc_sb, a.loc_sn = lc.data_ptr(), lc.stride(0), lc.stride(1)
+    if offsets is not None:
+        of = _inner_contig(_float(offsets), 2)
+        keep.append(of)
+        a.offsets, a.off_dtype = of.data_ptr(), _lib.DTYPE_CODE[of.dtype]
+        a.off_sb, a.off_sn, a.off_sh = of.stride(0), of.stride(1), of.stride(2)
+    if kv_pos is not None:
+        kp = _f32pos(kv_pos)
+        keep.append(kp)
+        a.kv_pos, a.kp_sb, a.kp_sn = kp.data_ptr(), kp.stride(0), kp.stride(1)
+    if attn is not None:
+        at = _inner_contig(_float(attn), 1)
+        keep.append(at)
+        a.attn, a.attn_dtype = at.data_ptr(), _lib.DTYPE_CODE[at.dtype]
+        a.at_sb, a.at_sn, a.at_sh = at.stride(0), at.stride(1), at.stride(2)
+    if weights is not None:
+        wt = _inner_contig(_float(weights), 2)
+        keep.append(wt)
+        a.weights, a.w_dtype = wt.data_ptr(), _lib.DTYPE_CODE[wt.dtype]
+        a.w_sb, a.w_sn, a.w_sh = wt.stride(0), wt.stride(1), wt.stride(2)
+    C = 0
+    vdtype = torch.float32
+    if values is not None:
+        v = values if values.dtype in _lib.DTYPE_CODE else values.to(torch.float32)
+        if v.stride(-1) != 1 or v.data_ptr() % 16 or any((st * v.element_size()) % 16 for st in v.stride()[:3]):
+            v = v.contiguous()
+        do = dout.to(v.dtype)
+        if do.stride(-1) != 1 or do.data_ptr() % 16 or any((st * do.element_size()) % 16 for st in do.stride()[:3]):
+            do = do.contiguous()
+        keep += [v, do]
+        C, vdtype = v.shape[-1], v.dtype
+        a.dtype, a.values = _lib.DTYPE_CODE[v.dtype], v.data_ptr()
+        a.v_sb, a.v_sn, a.v_sh = v.stride(0), v.stride(1), v.stride(2)
+        a.dout, a.do_sb, a.do_sn, a.do_sh = do.data_ptr(), do.stride(0), do.stride(1), do.stride(2)
+    a.C = C
+    if d_w_in is not None:
+        dw = _inner_contig(d_w_in.to(torch.float32), 2)
+        keep.append(dw)
+        a.d_w_in, a.dwi_sb, a.dwi_sn, a.dwi_sh = dw.data_ptr(), dw.stride(0), dw.stride(1), dw.stride(2)
+    pw = None
+    if power is not None:
+        pw = _power_ptr(power, dev)
+        keep.append(pw)
+        a.power = pw.data_ptr()
+    out = {}
+    f32 = dict(dtype=torch.float32, device=dev)
+    if want_loc:
+        out["d_loc"] = torch.empty((B, Q, H, S, D), **f32)
+        a.d_loc = out["d_loc"].data_ptr()
+    if want_attn:
+        out["d_attn"] = torch.empty((B, Q, H, S), **f32)
+        a.d_attn = out["d_attn"].data_ptr()
+    if want_weights:
+        out["d_weights"] = torch.empty((B, Q, H, S, K), **f32)
+        a.d_weights = out["d_weights"].data_ptr()
+    if want_kv:
+        out["d_kv_pos"] = torch.empty((B, Nkv, D), **f32)
+        a.d_kv_pos = out["d_kv_pos"].data_ptr()
+    if want_values:
+        out["d_values"] = torch.empty((B, Nkv, H, C), dtype=vdtype, device=dev)
+        a.d_values = out["d_values"].data_ptr()
+    if want_power:
+        out["d_power"] = torch.empty((1,), **f32)
+        a.d_power = out["d_power"].data_ptr()
+    ws_bytes = int(lib.aff_deform_bwd_workspace_bytes(ctypes.byref(a)))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    st = lib.aff_deform_bwd(ctypes.byref(a), ws.data_ptr(), ws_bytes, _lib.stream_ptr(dev))
+    _lib.check(st, "aff_deform_bwd")
+    return out
+
+
+def _power_grad(d_power, power):
+    if not torch.is_tensor(power):
+        return None
+    return d_power.reshape(power.shape).to(power.dtype)
+
+
 def _single_level(offsets, attn):
     B, N, H, K, _ = offsets.shape
     return offsets.reshape(B, N, H, 1, K, 2), attn.reshape(B, N, H, 1, K)
@@ -162,32 +287,86 @@ def fused_knn_deform_self_attn_forward_save(pos, offsets, attn_weights, values, 
     return fused_knn_deform_cross_attn_forward_save(pos, pos, offsets, attn_weights, values, power, D)
 
 
+def _save_power(ctx, power):
+    """Tensors go through save_for_backward; a Python number is kept as is."""
+    if torch.is_tensor(power):
+        ctx.power_num = None
+        return power
+    ctx.power_num = float(power)
+    return None
+
+
+def _knn_deform_backward(ctx, dout, query_pos, kv_pos, offsets, attn_weights, values, power, kidx, need):
+    """Gradients of the single-level fused KNN deformable attention (reference
+    fused_deform_attn.py:2661-2930): need = (qpos, kvpos, offsets, attn, values, power)."""
+    B, Nq, H, K, _ = offsets.shape
+    pw = power if power is not None else ctx.power_num
+    g = deform_backward_launch(
+        _lib.DEFORM_BWD_SHEPARD, dout, idx=kidx.reshape(B, Nq, H, K, kidx.shape[-1]), loc=query_pos,
+        offsets=offsets, kv_pos=kv_pos, attn=attn_weights, values=values, power=pw,
+        want_loc=need[0] or need[2], want_attn=need[3], want_kv=need[1], want_values=need[4],
+        want_power=need[5] and power is not None)
+    d_qpos = g["d_loc"].sum(dim=(2, 3)).to(query_pos.dtype) if need[0] else None
+    d_kv = g["d_kv_pos"].to(kv_pos.dtype) if need[1] else None
+    d_off = g["d_loc"].to(offsets.dtype) if need[2] else None
+    d_attn = g["d_attn"].to(attn_weights.dtype) if need[3] else None
+    d_val = g["d_values"].to(values.dtype) if need[4] else None
+    d_pow = _power_grad(g["d_power"], power) if "d_power" in g else None
+    return d_qpos, d_kv, d_off, d_attn, d_val, d_pow
+
+
 class FusedKNNDeformSelfAttnFunction(Function):
-    """Autograd entry (forward only: the backward kernels are not built yet)."""
+    """Autograd entry (reference fused_deform_attn.py:3981-4017): the forward keeps
+    the neighbour indices it found; backward returns (d_pos, d_offsets,
+    d_attn_weights, d_values, d_power, None) through aff_deform_bwd, where d_pos
+    sums the position's query and key roles."""
 
     @staticmethod
     @custom_fwd(device_type="cuda")
     def forward(ctx, pos, offsets, attn_weights, values, power, D=2):
-        return fused_knn_deform_self_attn_forward(pos, offsets, attn_weights, values, power, D)
+        assert D == 2, "Currently only D=2 is supported"
+        assert offsets.shape[3] == 4, "Currently only K=4 sampling points supported"
+        if not any(ctx.needs_input_grad[:5]):
+            return fused_knn_deform_self_attn_forward(pos, offsets, attn_weights, values, power, D)
+        out, kidx, _ = fused_knn_deform_self_attn_forward_save(pos, offsets, attn_weights, values, power, D)
+        ctx.save_for_backward(pos, offsets, attn_weights, values, kidx, _save_power(ctx, power))
+        return out
 
     @staticmethod
     @custom_bwd(device_type="cuda")
     def backward(ctx, dout):
-        raise NotImplementedError("deformable attention backward is not implemented in affmae_amd yet")
+        pos, offsets, attn_weights, values, kidx, power = ctx.saved_tensors
+        n = ctx.needs_input_grad
+        need = (n[0], n[0], n[1], n[2], n[3], n[4])
+        d_q, d_kv, d_off, d_attn, d_val, d_pow = _knn_deform_backward(ctx, dout, pos, pos, offsets, attn_weights,
+                                                                       values, power, kidx, need)
+        d_pos = (d_q + d_kv).to(pos.dtype) if n[0] else None
+        return d_pos, d_off, d_attn, d_val, d_pow, None
 
 
 class FusedKNNDeformCrossAttnFunction(Function):
-    """Autograd entry (forward only: the backward kernels are not built yet)."""
+    """Autograd entry (reference fused_deform_attn.py:4020-4056): backward returns
+    (d_query_pos, d_kv_pos, d_offsets, d_attn_weights, d_values, d_power, None)."""
 
     @staticmethod
     @custom_fwd(device_type="cuda")
     def forward(ctx, query_pos, kv_pos, offsets, attn_weights, values, power, D=2):
-        return fused_knn_deform_cross_attn_forward(query_pos, kv_pos, offsets, attn_weights, values, power, D)
+        assert D == 2, "Currently only D=2 is supported"
+        assert offsets.shape[3] == 4, "Currently only K=4 sampling points supported"
+        if not any(ctx.needs_input_grad[:6]):
+            return fused_knn_deform_cross_attn_forward(query_pos, kv_pos, offsets, attn_weights, values, power, D)
+        out, kidx, _ = fused_knn_deform_cross_attn_forward_save(query_pos, kv_pos, offsets, attn_weights, values,
+                                                                power, D)
+        ctx.save_for_backward(query_pos, kv_pos, offsets, attn_weights, values, kidx, _save_power(ctx, power))
+        return out
 
     @staticmethod
     @custom_bwd(device_type="cuda")
     def backward(ctx, dout):
-        raise NotImplementedError("deformable attention backward is not implemented in affmae_amd yet")
+        query_pos, kv_pos, offsets, attn_weights, values, kidx, power = ctx.saved_tensors
+        grads = _knn_deform_backward(ctx, dout, query_pos, kv_pos, offsets, attn_weights, values, power, kidx,
+                                     ctx.needs_input_grad[:6])
+        return (*grads, None)
 
 
 def fused_knn_deformable_self_attention(pos, offsets, attn_weights, values, power, D=2):
@@ -201,15 +380,55 @@ def fused_knn_deformable_cross_attention(query_pos, kv_pos, offsets, attn_weight
     return FusedKNNDeformCrossAttnFunction.apply(query_pos, kv_pos, offsets, attn_weights, values, power, D)
 
 
+class MSDeformAttnFunction(Function):
+    """Autograd entry of the multi-level form: backward returns the gradients of
+    (query_pos, kv_pos, offsets, attn, values, power) through aff_deform_bwd."""
+
+    @staticmethod
+    @custom_fwd(device_type="cuda")
+    def forward(ctx, query_pos, kv_pos, offsets, attn, values, power, level_start, k, mode):
+        ctx.level_start, ctx.mode = tuple(level_start), mode
+        if not any(ctx.needs_input_grad[:6]):
+            return deform_launch(query_pos, kv_pos, list(level_start), offsets, attn, values, power, k, mode)
+        out, kidx, _ = deform_launch(query_pos, kv_pos, list(level_start), offsets, attn, values, power, k, mode,
+                                     return_knn=True)
+        ctx.save_for_backward(query_pos, kv_pos, offsets, attn, values, kidx, _save_power(ctx, power))
+        return out
+
+    @staticmethod
+    @custom_bwd(device_type="cuda")
+    def backward(ctx, dout):
+        query_pos, kv_pos, offsets, attn, values, kidx, power = ctx.saved_tensors
+        n = ctx.needs_input_grad
+        B, Nq, H, L, P, _ = offsets.shape
+        pw = power if power is not None else ctx.power_num
+        mode = _lib.DEFORM_BWD_SHEPARD if ctx.mode == _lib.DEFORM_SHEPARD else _lib.DEFORM_BWD_IDW
+        g = deform_backward_launch(
+            mode, dout, idx=kidx.reshape(B, Nq, H, L * P, kidx.shape[-1]), loc=query_pos,
+            offsets=offsets.reshape(B, Nq, H, L * P, 2), kv_pos=kv_pos, attn=attn.reshape(B, Nq, H, L * P),
+            values=values, power=pw, level_start=ctx.level_start, P=P,
+            want_loc=n[0] or n[2], want_attn=n[3], want_kv=n[1], want_values=n[4], want_power=n[5] and power is not None)
+        d_q = g["d_loc"].sum(dim=(2, 3)).to(query_pos.dtype) if n[0] else None
+        d_kv = g["d_kv_pos"].to(kv_pos.dtype) if n[1] else None
+        d_off = g["d_loc"].reshape(offsets.shape).to(offsets.dtype) if n[2] else None
+        d_at = g["d_attn"].reshape(attn.shape).to(attn.dtype) if n[3] else None
+        d_val = g["d_values"].to(values.dtype) if n[4] else None
+        d_pow = _power_grad(g["d_power"], power) if "d_power" in g else None
+        return d_q, d_kv, d_off, d_at, d_val, d_pow, None, None, None
+
+
 def ms_deformable_attention(query_pos, kv_pos, level_start, offsets, attn, values, power=3.0, k=3,
                             weighting="idw", return_knn=False):
     """Multi-level deformable attention: each of the P points per level is
     interpolated from its k nearest points of that level by inverse-distance
     (``weighting='idw'``, weights 1/(d2^power + 1e-10) normalised) or Shepard
-    softmax weights, scaled by attn (softmaxed over levels x points)."""
+    softmax weights, scaled by attn (softmaxed over levels x points).
+    Differentiable in every float input (MSDeformAttnFunction)."""
     mode = _lib.DEFORM_IDW if weighting == "idw" else _lib.DEFORM_SHEPARD
-    return deform_launch(query_pos, kv_pos, list(level_start), offsets, attn, values, power, k, mode,
-                         return_knn=return_knn)
+    if return_knn:
+        return deform_launch(query_pos, kv_pos, list(level_start), offsets, attn, values, power, k, mode,
+                             return_knn=True)
+    return MSDeformAttnFunction.apply(query_pos, kv_pos, offsets, attn, values, power, tuple(level_start), k, mode)
 
 
 # -------------------------------------------------------- given indices ----
@@ -267,17 +486,33 @@ def fused_deform_attn_forward(sampling_locs, kv_pos, nb_idx, power, attn_weights
 
 
 class FusedDeformAttnFunction(Function):
-    """Autograd entry (forward only: the backward kernels are not built yet)."""
+    """Autograd entry (reference fused_deform_attn.py:654-690): backward returns
+    (d_sampling_locs, d_kv_pos, None, d_power, d_attn_weights, d_values, None, None)."""
 
     @staticmethod
     @custom_fwd(device_type="cuda")
     def forward(ctx, sampling_locs, kv_pos, nb_idx, power, attn_weights, values, D=2, use_heuristics=None):
-        return fused_deform_attn_forward(sampling_locs, kv_pos, nb_idx, power, attn_weights, values, D)
+        out = fused_deform_attn_forward(sampling_locs, kv_pos, nb_idx, power, attn_weights, values, D)
+        ctx.save_for_backward(sampling_locs, kv_pos, nb_idx, attn_weights, values, _save_power(ctx, power))
+        return out
 
     @staticmethod
     @custom_bwd(device_type="cuda")
     def backward(ctx, dout):
-        raise NotImplementedError("fused deformable attention backward is not implemented in affmae_amd yet")
+        sl, kv, nb_idx, attn, values, power = ctx.saved_tensors
+        n = ctx.needs_input_grad
+        B, N, K = nb_idx.shape
+        pw = power if power is not None else ctx.power_num
+        g = deform_backward_launch(
+            _lib.DEFORM_BWD_SAMPLE, dout.unsqueeze(2), idx=nb_idx.reshape(B, N, 1, 1, K), loc=sl, kv_pos=kv,
+            attn=attn.reshape(B, N, 1, 1), values=values.unsqueeze(2), power=pw,
+            want_loc=n[0], want_kv=n[1], want_power=n[3] and power is not None, want_attn=n[4], want_values=n[5])
+        d_sl = g["d_loc"].reshape(B, N, -1).to(sl.dtype) if n[0] else None
+        d_kv = g["d_kv_pos"].to(kv.dtype) if n[1] else None
+        d_pow = _power_grad(g["d_power"], power) if "d_power" in g else None
+        d_attn = g["d_attn"].reshape(attn.shape).to(attn.dtype) if n[4] else None
+        d_val = g["d_values"].reshape(values.shape).to(values.dtype) if n[5] else None
+        return d_sl, d_kv, None, d_pow, d_attn, d_val, None, None
 
 
 def fused_deformable_attention(sampling_locs, kv_pos, nb_idx, power, attn_weights, values, D=2, use_heuristics=None):

@@ -40,14 +40,34 @@ def launch_msdetrpc_forward(nn_idx, nn_weight, attn, val):
 
 
 class MSDETRPCFunction(Function):
-    """Autograd entry (forward only: the backward kernels are not built yet)."""
+    """Autograd entry (reference msdetrpc.py:372-390): backward returns
+    (None, d_nn_weight, d_attn, d_val) through aff_deform_bwd (GIVEN weights;
+    d_val is a fixed-order sum, no float atomics)."""
 
     @staticmethod
     @custom_fwd(device_type="cuda")
     def forward(ctx, nn_idx, nn_weight, attn, val):
+        ctx.save_for_backward(nn_idx, nn_weight, attn, val)
         return launch_msdetrpc_forward(nn_idx, nn_weight, attn, val)
 
     @staticmethod
     @custom_bwd(device_type="cuda")
     def backward(ctx, d_out):
-        raise NotImplementedError("MSDETRPC backward is not implemented in affmae_amd yet")
+        nn_idx, nn_weight, attn, val = ctx.saved_tensors
+        n = ctx.needs_input_grad
+        d_nw, d_att, d_val = launch_msdetrpc_backward(d_out, nn_idx, nn_weight, attn, val,
+                                                      want=(n[1], n[2], n[3]))
+        return None, d_nw, d_att, d_val
+
+
+def launch_msdetrpc_backward(d_out, nn_idx, nn_weight, attn, val, want=(True, True, True)):
+    """(d_nn_weight [B,N,M,K], d_attn [B,N,M], d_val [B,Nval,C]) (reference msdetrpc.py:328-369)."""
+    from .fused_deform_attn import deform_backward_launch
+    B, N, M, K = nn_idx.shape
+    g = deform_backward_launch(_lib.DEFORM_BWD_GIVEN, d_out.unsqueeze(2), idx=nn_idx.unsqueeze(2),
+                               weights=nn_weight.unsqueeze(2), attn=attn.unsqueeze(2), values=val.unsqueeze(2),
+                               want_weights=want[0], want_attn=want[1], want_values=want[2])
+    d_nw = g["d_weights"].reshape(nn_weight.shape).to(nn_weight.dtype) if want[0] else None
+    d_att = g["d_attn"].reshape(attn.shape).to(attn.dtype) if want[1] else None
+    d_val = g["d_values"].reshape(val.shape).to(val.dtype) if want[2] else None
+    return d_nw, d_att, d_val

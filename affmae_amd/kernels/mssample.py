@@ -10,7 +10,8 @@ from __future__ import annotations
 from torch.autograd import Function
 from torch.amp import custom_fwd, custom_bwd
 
-from .fused_deform_attn import deform_sample_launch
+from .. import _lib
+from .fused_deform_attn import _power_grad, _save_power, deform_backward_launch, deform_sample_launch
 
 
 def mssample_forward(sampling_locs, kv_pos, nb_idx, power, D=2):
@@ -22,17 +23,35 @@ def mssample_forward(sampling_locs, kv_pos, nb_idx, power, D=2):
 
 
 class MSSampleFunction(Function):
-    """Autograd entry (forward only: the backward kernel is not built yet)."""
+    """Autograd entry (reference mssample.py:402-449): backward returns
+    (d_sampling_locs, d_kv_pos, None, d_power, None) through aff_deform_bwd."""
 
     @staticmethod
     @custom_fwd(device_type="cuda")
     def forward(ctx, sampling_locs, kv_pos, nb_idx, power, D=2):
+        ctx.save_for_backward(sampling_locs, kv_pos, nb_idx, _save_power(ctx, power))
         return mssample_forward(sampling_locs, kv_pos, nb_idx, power, D)
 
     @staticmethod
     @custom_bwd(device_type="cuda")
     def backward(ctx, dout):
-        raise NotImplementedError("mssample backward is not implemented in affmae_amd yet")
+        sl, kv, nb_idx, power = ctx.saved_tensors
+        n = ctx.needs_input_grad
+        d_sl, d_kv, d_pow = mssample_backward(dout, sl, kv, nb_idx, power if power is not None else ctx.power_num,
+                                              want=(n[0], n[1], n[3] and power is not None))
+        return d_sl, d_kv, None, d_pow, None
+
+
+def mssample_backward(dout, sampling_locs, kv_pos, nb_idx, power, want=(True, True, True)):
+    """(d_sampling_locs, d_kv_pos, d_power) from dL/dweights [B,N,K(,1)] (reference mssample.py:345-399)."""
+    B, N, K = nb_idx.shape
+    g = deform_backward_launch(_lib.DEFORM_BWD_SAMPLE_SQ, None, idx=nb_idx.reshape(B, N, 1, 1, K),
+                               loc=sampling_locs, kv_pos=kv_pos, d_w_in=dout.reshape(B, N, 1, 1, K), power=power,
+                               want_loc=want[0], want_kv=want[1], want_power=want[2])
+    d_sl = g["d_loc"].reshape(B, N, -1).to(sampling_locs.dtype) if want[0] else None
+    d_kv = g["d_kv_pos"].to(kv_pos.dtype) if want[1] else None
+    d_pow = _power_grad(g["d_power"], power) if want[2] else None
+    return d_sl, d_kv, d_pow
 
 
 def mssample(sampling_locs, kv_pos, nb_idx, power, D=2):

@@ -399,6 +399,87 @@ aff_status aff_msdetrpc_fwd(const void *nn_idx, int idx_is_i64, int64_t i_sb, in
                             void *out, int64_t o_sb, int64_t o_sn, aff_stream_t stream);
 
 /* ------------------------------------------------------------------------ *
+ * Backward of the deformable gathers (all three forward entry points above).
+ *
+ * Replaces: fused_knn_deform_cross_attn_backward / _self_attn_backward
+ *           src/layers/kernels/fused_deform_attn.py:2661-2930 (kernels
+ *           :1521-2386), FusedKNNDeform{Self,Cross}AttnFunction.backward
+ *           :4002, :4041;  fused_deform_attn_backward :574-650 (kernel
+ *           :253-500), FusedDeformAttnFunction.backward :679;
+ *           mssample_backward  mssample.py:345-399 (kernel :142-298);
+ *           launch_msdetrpc_backward  msdetrpc.py:328-369 (kernels :133-300).
+ *
+ * One row r = (b, q, h) of dout [B, Q, H, C] holds S samples of K neighbours:
+ *   out[r] = sum_s attn[r, s] * sum_j w[r, s, j] * values[b, row(s, j), h]
+ * row(s, j) = level_start[s / P] + idx[r, s, j]; a pair is valid when
+ * idx >= 0 and row < level_start[s / P + 1] (invalid pairs carry no weight).
+ * Weights by `mode` (the forward's formulas, recomputed from positions:
+ * loc = loc[b, q] + offsets[r, s] (offsets NULL = 0), d2 = sum_d fl(diff_d^2),
+ * diff = loc - kv_pos[b, row], p = max(power, 1e-6)):
+ *   AFF_DEFORM_BWD_SHEPARD  softmax(-p (sqrt(d2) + 1e-6)), aff_deform_fwd SHEPARD
+ *   AFF_DEFORM_BWD_IDW      IDW on d2 with the raw power, aff_deform_fwd IDW
+ *   AFF_DEFORM_BWD_SAMPLE   softmax(-p (sqrt(d2) + 1e-6)), aff_deform_sample_fwd eps 0
+ *   AFF_DEFORM_BWD_SAMPLE_SQ softmax(-p sqrt(d2 + 1e-6)), aff_deform_sample_fwd eps 1
+ *   AFF_DEFORM_BWD_GIVEN    weights[r, s, j] as given (aff_msdetrpc_fwd)
+ * With g_j = dL/dw_j (= attn * <dout[r], values[b, row_j, h]>, or d_w_in when
+ * values is NULL), the distance modes follow the reference's chain rule:
+ * the softmax backward dlg_j = w_j (g_j - sum_i w_i g_i) treats the 1e-8 of
+ * the denominator as absent; d(loc) = sum_j dist'_j (diff_j) with
+ *   SHEPARD   -p dlg_j diff_j / (sqrt(d2_j) + 1e-6)
+ *   SAMPLE    -p dlg_j diff_j / max(sqrt(d2_j) + 1e-6 - 1e-6, 1e-8)
+ *   SAMPLE_SQ -p dlg_j diff_j / (sqrt(d2_j + 1e-6) + 1e-8)
+ *   IDW       2 diff_j dL/du_j du_j/dd2_j,  dL/du_j = (g_j - sum_i w_i g_i) / (sum u + 1e-12)
+ * and d(kv_pos[b, row_j]) gets the negated pair term; d_power = sum over
+ * pairs of dlg_j (-dist_j) (IDW: dL/du_j du_j/dpower, 0 where d2 == 0).
+ *
+ * Every scattered sum (d_values, d_kv_pos, d_power) is a fixed-order gather
+ * over pairs bucketed by a stable sort: the results are bitwise reproducible.
+ * Layouts: loc [B, Q, D] fp32 (D <= 4); offsets [B, Q, H, S, D] with (S, D)
+ * contiguous; idx [B, Q, H, S, K] int32/int64 with (S, K) contiguous; attn
+ * [B, Q, H, S] (S contiguous) or NULL = 1; weights / d_w_in [B, Q, H, S, K];
+ * kv_pos [B, Nkv, D] fp32; values [B, Nkv, H, C] and dout [B, Q, H, C] in
+ * `dtype`, unit stride on C, C % 8 == 0, C <= 2048, 16-byte aligned rows.
+ * Outputs (each NULL when not wanted, contiguous): d_loc [B, Q, H, S, D]
+ * fp32 (d_offsets; its sum over (h, s) is d(loc)), d_attn [B, Q, H, S] fp32,
+ * d_weights [B, Q, H, S, K] fp32 (GIVEN), d_kv_pos [B, Nkv, D] fp32,
+ * d_values [B, Nkv, H, C] in `dtype`, d_power one fp32.  K <= 16,
+ * B * Q * H * S * K < 2^31.  ws: aff_deform_bwd_workspace_bytes().
+ * ------------------------------------------------------------------------ */
+enum {
+    AFF_DEFORM_BWD_SHEPARD = 0,
+    AFF_DEFORM_BWD_IDW = 1,
+    AFF_DEFORM_BWD_SAMPLE = 2,
+    AFF_DEFORM_BWD_SAMPLE_SQ = 3,
+    AFF_DEFORM_BWD_GIVEN = 4
+};
+
+typedef struct aff_deform_bwd_args {
+    int mode;
+    int B, Q, H, S, K, C, D, P, Nkv;
+    int level_start[AFF_DEFORM_MAX_LEVELS + 1];
+    const float *loc; int64_t loc_sb, loc_sn;
+    const void *offsets; int off_dtype; int64_t off_sb, off_sn, off_sh;
+    const float *kv_pos; int64_t kp_sb, kp_sn;
+    const void *idx; int idx_is_i64; int64_t i_sb, i_sn, i_sh;
+    const void *attn; int attn_dtype; int64_t at_sb, at_sn, at_sh;
+    const void *weights; int w_dtype; int64_t w_sb, w_sn, w_sh;
+    int dtype;
+    const void *values; int64_t v_sb, v_sn, v_sh;
+    const void *dout; int64_t do_sb, do_sn, do_sh;
+    const float *d_w_in; int64_t dwi_sb, dwi_sn, dwi_sh;
+    const float *power;
+    float *d_loc;
+    float *d_attn;
+    float *d_weights;
+    float *d_kv_pos;
+    void *d_values;
+    float *d_power;
+} aff_deform_bwd_args;
+
+size_t aff_deform_bwd_workspace_bytes(const aff_deform_bwd_args *args);
+aff_status aff_deform_bwd(const aff_deform_bwd_args *args, void *ws, size_t ws_bytes, aff_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
  * Neighbourhood index construction of the encoder's BasicLayer.
  *
  * Replaces the torch gathers of BasicLayer.forward  src/layers/aff.py:452-465

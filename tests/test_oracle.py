@@ -503,3 +503,68 @@ def test_torch_path_gradients_match_finite_differences():
         return torch_path.gathered_attention(q, k, v, idx, 0.7, bias=bias, mask=mask, blank_k=bk, blank_v=bv)
 
     assert torch.autograd.gradcheck(f, (q, k, v, table, bk, bv), eps=1e-6, atol=1e-7, rtol=1e-5)
+
+
+def _deform_case(mode, seed, with_values=True):
+    """Well-separated fp64 inputs (distances ~1..50) for the backward oracle pin."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    B, Q, H, S, K, D, Nkv, C = 2, 5, 2, 3, 4, 2, 20, 8
+    kv = (torch.rand(B, Nkv, D, generator=g, dtype=torch.float64) * 50)
+    loc = (torch.rand(B, Q, H, S, D, generator=g, dtype=torch.float64) * 50)
+    rows = torch.randint(0, Nkv, (B, Q, H, S, K), generator=g)
+    rows[0, 1, 0, 2, 3] = -1
+    rows[1, 3, 1, 0, 0] = -1
+    attn = torch.rand(B, Q, H, S, generator=g, dtype=torch.float64)
+    weights = torch.rand(B, Q, H, S, K, generator=g, dtype=torch.float64) if mode == "given" else None
+    values = torch.randn(B, Nkv, H, C, generator=g, dtype=torch.float64) if with_values else None
+    dout = torch.randn(B, Q, H, C, generator=g, dtype=torch.float64)
+    d_w_in = None if with_values else torch.randn(B, Q, H, S, K, generator=g, dtype=torch.float64)
+    power = 0.7 if mode != "idw" else 1.5
+    return loc, kv, rows, attn, weights, values, dout, d_w_in, power
+
+
+@pytest.mark.parametrize("mode,with_values", [("shepard", True), ("sample", True), ("sample_sq", False),
+                                               ("sample_sq", True), ("idw", True), ("given", True)])
+def test_deform_backward_oracle_matches_autograd(mode, with_values):
+    """oracle/deform_bwd.py (the reference's hand-written chain rule) against torch
+    autograd of the fp64 forward composition: every gradient, including d_power."""
+    import torch
+    from oracle import deform_bwd as ob
+    loc, kv, rows, attn, weights, values, dout, d_w_in, power = _deform_case(mode, 3, with_values)
+    leaves = {"loc": loc, "kv": kv, "attn": attn, "values": values, "weights": weights,
+              "power": torch.tensor(power, dtype=torch.float64)}
+    leaves = {k: (v.clone().requires_grad_(True) if v is not None else None) for k, v in leaves.items()}
+    out = ob.forward(mode, leaves["loc"], leaves["kv"], rows, leaves["power"], attn=leaves["attn"] if with_values else None,
+                     weights=leaves["weights"], values=leaves["values"])
+    L = (out * (dout if with_values else d_w_in)).sum()
+    L.backward()
+    ref = ob.deform_backward(mode, dout, loc, kv, rows, power, attn=attn, weights=weights, values=values,
+                             d_w_in=d_w_in)
+
+    def close(a, b, what):
+        scale = max(float(b.abs().max()), 1e-30)
+        assert float((a - b).abs().max()) <= 1e-6 * scale, f"{mode} {what}"
+
+    if mode != "given":
+        close(ref["d_loc"], leaves["loc"].grad, "d_loc")
+        close(ref["d_kv_pos"], leaves["kv"].grad, "d_kv_pos")
+        close(ref["d_power"], leaves["power"].grad, "d_power")
+    else:
+        close(ref["d_weights"], leaves["weights"].grad, "d_weights")
+    if with_values:
+        close(ref["d_attn"], leaves["attn"].grad, "d_attn")
+        close(ref["d_values"], leaves["values"].grad, "d_values")
+
+
+def test_deform_backward_oracle_catches_a_planted_sign_error(monkeypatch):
+    """A flipped sign in the position term fails the autograd pin (the check has teeth)."""
+    import torch
+    from oracle import deform_bwd as ob
+    loc, kv, rows, attn, weights, values, dout, d_w_in, power = _deform_case("shepard", 5)
+    ref = ob.deform_backward("shepard", dout, loc, kv, rows, power, attn=attn, values=values)
+    lg = loc.clone().requires_grad_(True)
+    (ob.forward("shepard", lg, kv, rows, power, attn=attn, values=values) * dout).sum().backward()
+    scale = float(lg.grad.abs().max())
+    assert float((ref["d_loc"] - lg.grad).abs().max()) <= 1e-6 * scale
+    assert float((-ref["d_loc"] - lg.grad).abs().max()) > 1e-2 * scale
