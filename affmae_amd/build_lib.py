@@ -41,6 +41,7 @@ EXTRA_FLAGS = {
     # Distances must be the un-fused fp32 value; the kernel also pins this
     # with a scoped pragma.
     "knn.hip": ["-ffp-contract=off"],
+    "knn_brute.hip": ["-ffp-contract=off"],
     # MFMA results in VGPRs: the attention kernels read every S element with VALU
     # ops, which an AGPR destination would precede with a copy.
     "nbhd_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],

@@ -26,6 +26,7 @@
 // "next smallest key" passes.  knn_query_kernel (one lane per query, global
 // grid only) serves k > 64 and images of more than 65536 points.
 #include "grid2d.hpp"
+#include "knn_brute.hpp"
 
 #include <limits.h>
 
@@ -804,8 +805,8 @@ size_t knn_grid_bytes(int B, int N) {
 }  // namespace
 
 extern "C" size_t aff_knn_workspace_bytes(int B, int M, int N, int D, int k) {
-    (void)D; (void)k;
-    if (B <= 0 || N <= 0) return 0;
+    (void)k;
+    if (B <= 0 || N <= 0 || D != 2) return 0;  // the search in other dimensions needs no workspace
     return knn_grid_bytes(B, N) + grid::align256(sizeof(float4) * (size_t)B * (size_t)(M > 0 ? M : 0));
 }
 
@@ -816,10 +817,13 @@ extern "C" aff_status aff_knn(const float *query, int64_t q_sb, int64_t q_sm, co
     AFF_CHECK_ARG(B >= 0 && M >= 0, "aff_knn: B=%d and M=%d must be >= 0", B, M);
     AFF_CHECK_ARG(N >= 1, "aff_knn: N=%d must be >= 1", N);
     AFF_CHECK_ARG(k >= 1 && k <= N, "aff_knn: k=%d exceeds number of reference points N=%d (or k < 1)", k, N);
-    if (D != 2) return fail(AFF_ERR_UNSUPPORTED, "aff_knn: D=%d not supported (only D=2)", D);
+    if (D < 1 || D > 4) return fail(AFF_ERR_UNSUPPORTED, "aff_knn: D=%d not supported (1 <= D <= 4)", D);
     AFF_CHECK_ARG(q_sb >= 0 && q_sm >= 0 && r_sb >= 0 && r_sn >= 0, "aff_knn: negative stride");
     if (B == 0 || M == 0) return AFF_OK;
     AFF_CHECK_ARG(query && ref && out_idx, "aff_knn: NULL query/ref/out_idx");
+    if (D != 2)
+        return knn_brute_launch(query, q_sb, q_sm, ref, r_sb, r_sn, B, M, N, D, k, out_idx, idx_is_i64, out_d2,
+                                static_cast<hipStream_t>(stream));
     const grid::Segs s = grid::make_segs(1, &N);
     const grid::WsLayout L = grid::ws_layout(B, s);
     const size_t need = aff_knn_workspace_bytes(B, M, N, D, k);
@@ -929,7 +933,7 @@ extern "C" aff_status aff_knn_noalloc(const float *query, int64_t q_sb, int64_t 
     AFF_CHECK_ARG(B >= 0 && M >= 0, "aff_knn_noalloc: B=%d and M=%d must be >= 0", B, M);
     AFF_CHECK_ARG(N >= 1, "aff_knn_noalloc: N=%d must be >= 1", N);
     AFF_CHECK_ARG(k >= 1 && k <= N, "aff_knn_noalloc: k=%d exceeds number of reference points N=%d (or k < 1)", k, N);
-    if (D != 2) return fail(AFF_ERR_UNSUPPORTED, "aff_knn_noalloc: D=%d not supported (only D=2)", D);
+    if (D < 1 || D > 4) return fail(AFF_ERR_UNSUPPORTED, "aff_knn_noalloc: D=%d not supported (1 <= D <= 4)", D);
     AFF_CHECK_ARG(q_sb >= 0 && q_sm >= 0 && r_sb >= 0 && r_sn >= 0, "aff_knn_noalloc: negative stride");
     if (B == 0 || M == 0) return AFF_OK;
     AFF_CHECK_ARG(query && ref && out_idx, "aff_knn_noalloc: NULL query/ref/out_idx");

@@ -27,15 +27,15 @@ def _as_f32(t: torch.Tensor) -> torch.Tensor:
 
 
 def _require_2d(D: int) -> None:
-    """The reference accepts D in {2, 3, 4}; only the 2-D search (every model caller's
-    case: token coordinates) is built here."""
-    if D != 2:
-        raise NotImplementedError(f"affmae_amd KNN is built for 2-D coordinates only (got D={D})")
+    """The reference accepts D in {2, 3, 4}: D = 2 runs the grid-bucketed search,
+    D = 3 / 4 the brute-force exact search (k <= 64)."""
+    if D not in (1, 2, 3, 4):
+        raise NotImplementedError(f"affmae_amd KNN supports 1 <= D <= 4 (got D={D})")
 
 
 def knn_launch(query: torch.Tensor, ref: torch.Tensor, k: int, out_dtype=torch.int32,
                return_dist: bool = False):
-    """Call aff_knn on [B,M,2] / [B,N,2] fp32 views; returns idx (and d2)."""
+    """Call aff_knn on [B,M,D] / [B,N,D] fp32 views; returns idx (and d2)."""
     lib = _lib.load()
     dev = _lib.require_cuda(query, ref)
     _require_2d(query.shape[-1])

@@ -41,7 +41,7 @@ const char *aff_last_error(void);
 int aff_abi_version(void);
 
 /* ------------------------------------------------------------------------ *
- * Exact K-nearest-neighbour search over 2-D points.
+ * Exact K-nearest-neighbour search over 2-D (and 1-, 3-, 4-D) points.
  *
  * Replaces: knn_forward()  src/layers/kernels/knn.py:1368-1540
  *           (and its k>8 fallback knn_large_k_fallback() knn.py:1335-1365)
@@ -55,7 +55,12 @@ int aff_abi_version(void);
  * finite coordinates.  out_idx is [B, M, k] contiguous, int32 or int64
  * (idx_is_i64 != 0).  out_d2 ([B, M, k] fp32) may be NULL.
  * ws must hold aff_knn_workspace_bytes(B, M, N, D, k) bytes.
- * Only D == 2 is implemented; other D return AFF_ERR_UNSUPPORTED.
+ * D == 2 runs the grid-bucketed search (any k).  D == 1, 3 or 4 (the
+ * reference's D = 3 / 4 kernels, knn.py:340-419, 474-581) runs an exact
+ * brute-force search with k <= 64 and no workspace; query / ref then hold D
+ * coordinates per point (unit stride) and the sum of squares runs over the
+ * dimensions in order.  Other D, or k > 64 with D != 2, return
+ * AFF_ERR_UNSUPPORTED.
  * ------------------------------------------------------------------------ */
 size_t aff_knn_workspace_bytes(int B, int M, int N, int D, int k);
 

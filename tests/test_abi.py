@@ -73,8 +73,11 @@ def test_knn_validation(lib):
     st = lib.aff_knn(DUMMY, 20, 2, DUMMY, 40, 2, 2, 10, 20, 2, 21, DUMMY, 0, None, DUMMY, ws, None)
     assert st == _lib.AFF_ERR_INVALID_ARG
     assert b"exceeds number of reference points" in lib.aff_last_error()
-    # unsupported D
-    st = lib.aff_knn(DUMMY, 30, 3, DUMMY, 60, 3, 2, 10, 20, 3, 4, DUMMY, 0, None, DUMMY, ws, None)
+    # unsupported D, and k > 64 outside 2-D
+    st = lib.aff_knn(DUMMY, 50, 5, DUMMY, 100, 5, 2, 10, 20, 5, 4, DUMMY, 0, None, DUMMY, ws, None)
+    assert st == _lib.AFF_ERR_UNSUPPORTED
+    assert lib.aff_knn_workspace_bytes(2, 10, 100, 3, 65) == 0
+    st = lib.aff_knn(DUMMY, 300, 3, DUMMY, 300, 3, 2, 10, 100, 3, 65, DUMMY, 0, None, None, 0, None)
     assert st == _lib.AFF_ERR_UNSUPPORTED
     # missing / short workspace
     st = lib.aff_knn(DUMMY, 20, 2, DUMMY, 40, 2, 2, 10, 20, 2, 4, DUMMY, 0, None, None, 0, None)

@@ -163,3 +163,37 @@ def test_reference_fallback_names(oracle_mod, dev):
     np.testing.assert_array_equal(idx.cpu().numpy(), oih)
     np.testing.assert_allclose(dist.cpu().numpy(), np.sqrt(odh.astype(np.float64)), rtol=1e-6)
     np.testing.assert_array_equal(knn_keops(q.to(dev), pos.to(dev), 20).cpu().numpy(), oi)
+
+
+@pytest.mark.parametrize("D", [1, 3, 4])
+@pytest.mark.parametrize("k", [1, 4, 8, 13, 16, 32, 48, 64])
+def test_other_dims_bruteforce(oracle_mod, dev, D, k):
+    """D = 1 / 3 / 4 (the brute-force search): bit-exact indices and squared distances."""
+    g = torch.Generator().manual_seed(D * 100 + k)
+    ref = torch.rand(2, 1500, D, generator=g)
+    q = torch.rand(2, 700, D, generator=g)
+    _check(q, ref, k, oracle_mod, dev)
+
+
+@pytest.mark.parametrize("D", [3, 4])
+def test_other_dims_lattice_ties(oracle_mod, dev, D):
+    """Integer lattice with duplicated points: many equal distances, ties to the lower index."""
+    g = torch.Generator().manual_seed(D)
+    ref = torch.randint(0, 4, (2, 900, D), generator=g).float()
+    q = torch.randint(0, 4, (2, 300, D), generator=g).float() + 0.5 * (torch.rand(2, 300, D, generator=g) > 0.5)
+    for k in (8, 24):
+        _check(q, ref, k, oracle_mod, dev, out_dtype=torch.int32)
+
+
+def test_other_dims_reference_names(oracle_mod, dev):
+    """knn / knn_forward accept D = 3 and 4 like the reference's dispatch (knn.py:1368-1540)."""
+    g = torch.Generator().manual_seed(9)
+    ref = torch.rand(1, 400, 3, generator=g)
+    q = torch.rand(1, 100, 3, generator=g)
+    oi, _ = oracle_mod.knn(q.numpy(), ref.numpy(), 6)
+    np.testing.assert_array_equal(knn(q.to(dev), ref.to(dev), 6).cpu().numpy(), oi)
+    out = knn_forward(q.to(dev), ref.to(dev), 6, D=3)
+    assert out.dtype == torch.int32
+    np.testing.assert_array_equal(out.cpu().numpy().astype(np.int64), oi)
+    with pytest.raises(NotImplementedError):
+        knn(q.to(dev), ref.to(dev), 65)

@@ -41,6 +41,18 @@ def test_knn_matches_kdtree(oracle_mod, k):
         np.testing.assert_allclose(np.sqrt(d2[b]), dd.reshape(300, k), rtol=1e-5, atol=1e-7)
 
 
+@pytest.mark.parametrize("D,k", [(1, 5), (3, 8), (3, 40), (4, 16)])
+def test_knn_other_dims_match_kdtree(oracle_mod, D, k):
+    rng = np.random.default_rng(100 + D * k)
+    ref = rng.random((2, 500, D), dtype=np.float32)
+    q = rng.random((2, 200, D), dtype=np.float32)
+    idx, d2 = oracle_mod.knn(q, ref, k)
+    for b in range(2):
+        dd, ii = cKDTree(ref[b].astype(np.float64)).query(q[b].astype(np.float64), k=k)
+        np.testing.assert_array_equal(idx[b], ii.reshape(200, k))
+        np.testing.assert_allclose(np.sqrt(d2[b]), dd.reshape(200, k), rtol=1e-5, atol=1e-7)
+
+
 def test_knn_lattice_ties_known_answer(oracle_mod):
     # 5x5 lattice, indices row-major; query at the centre (2,2) = index 12.
     g = np.stack(np.meshgrid(np.arange(5), np.arange(5), indexing="xy"), -1).reshape(1, 25, 2).astype(np.float32)
