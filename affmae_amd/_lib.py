@@ -24,7 +24,7 @@ AFF_F32, AFF_F16, AFF_BF16 = 0, 1, 2
 KNN_NOALLOC_SCRATCH_BYTES = 16 << 20   # AFF_KNN_NOALLOC_SCRATCH_BYTES
 DTYPE_CODE = {torch.float32: AFF_F32, torch.float16: AFF_F16, torch.bfloat16: AFF_BF16}
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 P = ctypes.c_void_p
 I32 = ctypes.c_int
@@ -114,6 +114,29 @@ class DeformBwdArgs(ctypes.Structure):
     ]
 
 
+SFC_MAX_LEVELS = 16
+SFC_SCANLINE, SFC_PEANO, SFC_HILBERT = 0, 1, 2
+
+
+class SfcCurveArgs(ctypes.Structure):
+    """Mirror of ``aff_sfc_curve_args`` (include/affmae.h)."""
+    _fields_ = [
+        ("pos", P), ("p_sb", I64), ("p_sn", I64),
+        ("B", I32), ("N", I32), ("curve", I32), ("w", I32), ("levels", I32), ("first_w", I32),
+        ("cur_h", F32 * SFC_MAX_LEVELS), ("inv_h", F32 * SFC_MAX_LEVELS), ("level_scale", F32 * SFC_MAX_LEVELS),
+        ("keys", P),
+    ]
+
+
+class SfcAnchorArgs(ctypes.Structure):
+    """Mirror of ``aff_sfc_anchor_args`` (include/affmae.h)."""
+    _fields_ = [
+        ("pos", P), ("p_sb", I64), ("p_sn", I64),
+        ("B", I32), ("N", I32), ("plw", F32), ("plh", F32), ("npw", I32), ("ncell", I32),
+        ("cell_rank", P), ("prev_c", P), ("next_c", P), ("keys", P),
+    ]
+
+
 # Every symbol include/affmae.h declares, with (restype, argtypes).
 SIGNATURES = {
     "aff_last_error": (ctypes.c_char_p, []),
@@ -145,6 +168,11 @@ SIGNATURES = {
                                   I32, I32, I32, I32, I32, I32, P, I32, P, P, I32, P]),
     "aff_deform_bwd_workspace_bytes": (SZ, [ctypes.POINTER(DeformBwdArgs)]),
     "aff_deform_bwd": (I32, [ctypes.POINTER(DeformBwdArgs), P, SZ, P]),
+    "aff_sfc_curve_keys": (I32, [ctypes.POINTER(SfcCurveArgs), P]),
+    "aff_sfc_anchor_workspace_bytes": (SZ, [I32, I32]),
+    "aff_sfc_anchor_keys": (I32, [ctypes.POINTER(SfcAnchorArgs), P, SZ, P]),
+    "aff_sfc_argsort_workspace_bytes": (SZ, [I32, I32]),
+    "aff_sfc_argsort": (I32, [P, I32, I32, P, P, SZ, P]),
     "aff_layer_norm_fwd": (I32, [P, I32, I64, P, I32, I64, P, P, I64, I32, F32, P]),
     "aff_layer_norm_map_fwd": (I32, [P, I32, P, I32, P, P, P, I32, I32, I32, I32, I32, I32, I32, F32, P]),
 }

@@ -42,6 +42,8 @@ EXTRA_FLAGS = {
     # with a scoped pragma.
     "knn.hip": ["-ffp-contract=off"],
     "knn_brute.hip": ["-ffp-contract=off"],
+    # The curve and anchor keys reproduce torch's separately rounded products and sums.
+    "sfc.hip": ["-ffp-contract=off"],
     # MFMA results in VGPRs: the attention kernels read every S element with VALU
     # ops, which an AGPR destination would precede with a copy.
     "nbhd_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],

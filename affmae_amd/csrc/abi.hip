@@ -39,4 +39,4 @@ int device_cu_count() {
 
 extern "C" const char *aff_last_error(void) { return aff::g_last_error; }
 
-extern "C" int aff_abi_version(void) { return 7; }
+extern "C" int aff_abi_version(void) { return 8; }

@@ -4,7 +4,8 @@
 work; ``upsample_feature_shepard`` (geometry.py:97-167) runs the HIP KNN and
 weighted-gather kernels; ``space_filling_cluster`` (geometry.py:170-319) is
 the token ordering and balanced clustering the encoder runs before every
-stage's attention blocks (aff.py:436-446), torch ops as in the reference.
+stage's attention blocks (aff.py:436-446): its curve keys and sort run on
+the HIP kernels (aff_sfc_*), the gathers and cluster means are torch.
 """
 from __future__ import annotations
 
@@ -81,24 +82,104 @@ def _scanline_rank(nh: int, nw: int, width: int, device) -> torch.Tensor:
     return rank, order
 
 
+def _anchor_grid(n, m, h, w, sf_type):
+    """Patch grid of the anchor ordering (geometry.py:203-216): (rows, cols, row
+    height, column width); Peano / Hilbert round the rows to a power of 3 / 2."""
+    k = int(math.ceil(n / m))
+    patch_len = (h * w / k) ** 0.5
+    nph = int(round(h / patch_len))
+    npw = int(round(w / patch_len))
+    plh, plw = h / nph, w / npw
+    if sf_type in ("peano", "hilbert"):
+        base = 3 if sf_type == "peano" else 2
+        nph = max(base, int(base ** round(math.log(nph, base))))
+        plh = h / nph
+        npw = int(round(w / h * base) * (nph / base))
+        plw = w / npw
+    return nph, npw, plh, plw
+
+
+def _neighbour_centres(ordered_grid, plw, plh, dev):
+    """Patch centres in curve order and those of the previous / next patch on the
+    curve, extrapolated at both ends (geometry.py:238-248)."""
+    plhw = torch.tensor([plw, plh], dtype=torch.float32, device=dev)
+    centres = ordered_grid * plhw + plhw / 2 - 0.5
+    npch = centres.shape[0]
+    prev_c = torch.zeros_like(centres)
+    prev_c[1:] = centres[:npch - 1]
+    prev_c[0] = prev_c[1] - (prev_c[2] - prev_c[1])
+    next_c = torch.zeros_like(centres)
+    next_c[:npch - 1] = centres[1:]
+    next_c[-1] = next_c[-2] + (next_c[-2] - next_c[-3])
+    return plhw, prev_c, next_c
+
+
+def _ranking_hip(pos, m, h, w, sf_type, use_anchor):
+    """pos_ranking [b,n,1] of GPU tokens: curve / anchor keys and the argsort on the HIP kernels."""
+    from ..kernels import sfc
+    b, n, _ = pos.shape
+    dev = pos.device
+    curve = sfc.CURVES[sf_type]
+    if not use_anchor:
+        return sfc.argsort(sfc.curve_keys(pos, curve, h, w)).unsqueeze(2)
+    nph, npw, plh, plw = _anchor_grid(n, m, h, w, sf_type)
+    ys, xs = torch.meshgrid(torch.arange(nph, device=dev), torch.arange(npw, device=dev), indexing="ij")
+    grid = torch.stack([xs, ys], dim=2).reshape(-1, 2)
+    if curve == sfc.CURVES[""]:
+        rank, order = _scanline_rank(nph, npw, w, dev)
+    else:
+        order = sfc.argsort(sfc.curve_keys(grid.float().unsqueeze(0), curve, nph, npw))[0]
+        rank = torch.empty_like(order)
+        rank[order] = torch.arange(order.numel(), device=dev)
+    _, prev_c, next_c = _neighbour_centres(grid[order], plw, plh, dev)
+    keys = sfc.anchor_keys(pos, plw, plh, npw, rank, prev_c, next_c)
+    return sfc.argsort(keys).unsqueeze(2)
+
+
+def _ranking_torch(pos, m, h, w, use_anchor):
+    """pos_ranking [b,n,1] of CPU tokens along the scanline curve (the host-side
+    ordering of synthetic inputs; GPU tokens take the HIP kernels)."""
+    b, n, d = pos.shape
+    dev = pos.device
+    if use_anchor:
+        nph, npw, plh, plw = _anchor_grid(n, m, h, w, "")
+        rank, order = _scanline_rank(nph, npw, w, dev)
+        ys, xs = torch.meshgrid(torch.arange(nph, device=dev), torch.arange(npw, device=dev), indexing="ij")
+        grid = torch.stack([xs, ys], dim=2).reshape(-1, 2)[order]          # cells in curve order
+        plhw, prev_c, next_c = _neighbour_centres(grid, plw, plh, dev)
+        cell = (pos / plhw).floor()
+        cell = (cell[..., 0] + cell[..., 1] * npw).long()                  # row-major patch id
+        prank = rank.unsqueeze(0).expand(b, -1).gather(1, cell)             # b x n
+        d_prev = (pos - prev_c[prank]).pow(2).sum(-1)
+        d_next = (pos - next_c[prank]).pow(2).sum(-1)
+        ratio = d_prev / (d_next + 1e-5)
+        key = prank.unsqueeze(2) * (ratio.max() + 1) + ratio.unsqueeze(2)
+        return key.sort(dim=1, stable=True)[1]
+    rank, _ = _scanline_rank(h, w, w, dev)
+    pid = (pos[..., 0] + pos[..., 1] * w).long().reshape(-1)
+    return rank.gather(0, pid).reshape(b, n).sort(stable=True)[1].unsqueeze(2)
+
+
 def space_filling_cluster(pos, m, h, w, no_reorder=False, sf_type="", use_anchor=True):
     """Balanced clustering along a space-filling curve (geometry.py:170-319).
 
     pos [b,n,2] token positions (x, y) on an h x w canvas, m the cluster size.
     With anchors (the default, used by the encoder) the canvas is cut into
-    ~n/m patches visited along alternating horizontal scanlines; a token's
-    rank is its patch's rank, ties inside a patch broken by the ratio of its
-    squared distances to the previous and next patch centres
-    (geometry.py:199-268).  Returns, like the reference,
+    ~n/m patches visited along the curve (alternating horizontal scanlines
+    for sf_type '', or the Peano / Hilbert curve); a token's rank is its
+    patch's rank, ties inside a patch broken by the ratio of its squared
+    distances to the previous and next patch centres (geometry.py:199-268).
+    Without anchors the tokens themselves are ordered along the curve.  Keys
+    and sort run on the HIP kernels for GPU tokens (equal keys keep the lower
+    token index first); CPU tokens (synthetic input generation) are ordered
+    by torch along the scanline curve.  Returns, like the reference,
       no_reorder=False: (pos reordered, cluster_mean_pos [b,k,2],
                          member_idx [b,k,m], cluster_mask [b,k,m] or None,
                          pos_ranking [b,n,1])
       no_reorder=True:  (cluster_mean_pos, member_idx, cluster_mask)
-    Only the scanline curve (sf_type '') is built; 'peano' and 'hilbert'
-    raise NotImplementedError.
     """
-    if sf_type in ("peano", "hilbert"):
-        raise NotImplementedError(f"space_filling_cluster: sf_type={sf_type!r} is not built")
+    if sf_type not in ("", "peano", "hilbert"):
+        sf_type = ""          # the reference treats every other value as the scanline curve
     with torch.no_grad():
         pos = pos.detach()
         if pos.dtype != torch.float:
@@ -106,35 +187,12 @@ def space_filling_cluster(pos, m, h, w, no_reorder=False, sf_type="", use_anchor
         b, n, d = pos.shape
         k = int(math.ceil(n / m))
         dev = pos.device
-        if use_anchor:
-            patch_len = (h * w / k) ** 0.5
-            nph = int(round(h / patch_len))
-            npw = int(round(w / patch_len))
-            plh, plw = h / nph, w / npw
-            rank, order = _scanline_rank(nph, npw, w, dev)
-            ys, xs = torch.meshgrid(torch.arange(nph, device=dev), torch.arange(npw, device=dev), indexing="ij")
-            grid = torch.stack([xs, ys], dim=2).reshape(-1, 2)[order]          # cells in curve order
-            plhw = torch.tensor([plw, plh], dtype=torch.float32, device=dev)
-            centres = grid * plhw + plhw / 2 - 0.5
-            npch = centres.shape[0]
-            prev_c = torch.zeros_like(centres)
-            prev_c[1:] = centres[:npch - 1]
-            prev_c[0] = prev_c[1] - (prev_c[2] - prev_c[1])
-            next_c = torch.zeros_like(centres)
-            next_c[:npch - 1] = centres[1:]
-            next_c[-1] = next_c[-2] + (next_c[-2] - next_c[-3])
-            cell = (pos / plhw).floor()
-            cell = (cell[..., 0] + cell[..., 1] * npw).long()                  # row-major patch id
-            prank = rank.unsqueeze(0).expand(b, -1).gather(1, cell)             # b x n
-            d_prev = (pos - prev_c[prank]).pow(2).sum(-1)
-            d_next = (pos - next_c[prank]).pow(2).sum(-1)
-            ratio = d_prev / (d_next + 1e-5)
-            key = prank.unsqueeze(2) * (ratio.max() + 1) + ratio.unsqueeze(2)
-            pos_ranking = key.sort(dim=1)[1]                                     # b x n x 1
+        if pos.is_cuda:
+            pos_ranking = _ranking_hip(pos, m, h, w, sf_type, use_anchor)
         else:
-            rank, _ = _scanline_rank(h, w, w, dev)
-            pid = (pos[..., 0] + pos[..., 1] * w).long().reshape(-1)
-            pos_ranking = rank.gather(0, pid).reshape(b, n).sort()[1].unsqueeze(2)
+            if sf_type:
+                raise NotImplementedError("space_filling_cluster: Peano / Hilbert orders run on GPU tokens only")
+            pos_ranking = _ranking_torch(pos, m, h, w, use_anchor)
 
         pos = pos.gather(1, pos_ranking.expand(-1, -1, d))
         if k * m == n:

@@ -546,6 +546,64 @@ aff_status aff_layer_norm_map_fwd(const void *x, int x_dtype, void *y, int y_dty
                                   const float *bias, const float *keep, int cell, int B, int C, int H, int W,
                                   int token_major, int gelu, float eps, aff_stream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * Space-filling-curve ordering of tokens (the balanced clustering's sort keys).
+ *
+ * Replaces the key computation and sort of space_filling_cluster
+ * (src/utils/geometry.py:199-288) and calculate_peano_order /
+ * calculate_hilbert_order (geometry.py:322-460).
+ *
+ * aff_sfc_curve_keys: keys[b, n] (fp32) of pos[b, n] (fp32 (x, y), strides
+ * p_sb, p_sn, unit stride on the coordinate) along
+ *   AFF_SFC_SCANLINE  rows alternating in direction: id = trunc(x + y * w),
+ *                     key = (row odd ? w - 1 - col : col) + row * w
+ *   AFF_SFC_PEANO / AFF_SFC_HILBERT  `levels` base-3 / base-2 digit levels;
+ *                     digit_l = floor(rem * inv_h[l]), rem = fmod(rem, cur_h[l])
+ *                     (cur_h[l] the reference's h / base^(l+1) rounded to fp32,
+ *                     inv_h[l] = 1 / cur_h[l] in fp32), digits outside the
+ *                     canvas clamped; first_w > 0 selects the reference's wide
+ *                     first level (Peano only); key = order[L-1] + sum_l
+ *                     order[l] * level_scale[l] in fp32, in order of l.
+ * aff_sfc_anchor_keys: keys[b, n] = rank * (max ratio + 1) + ratio with the
+ *   patch of pos = (floor(x / plw), floor(y / plh)), cell = px + py * npw
+ *   (clamped to [0, ncell)), rank = cell_rank[cell], ratio = |pos - prev|^2
+ *   / (|pos - next|^2 + 1e-5), prev / next = prev_c / next_c[rank] (fp32
+ *   [ncell, 2], the centres of the neighbouring patches on the curve), the
+ *   maximum over all b, n.  ws: aff_sfc_anchor_workspace_bytes(B, N).
+ * aff_sfc_argsort: ranking[b, i] (int64) = the index of the token of rank i in
+ *   row b of keys [B, N] (fp32, contiguous), ascending, ties to the lower
+ *   index.  ws: aff_sfc_argsort_workspace_bytes(B, N).
+ * ------------------------------------------------------------------------ */
+#define AFF_SFC_MAX_LEVELS 16
+enum { AFF_SFC_SCANLINE = 0, AFF_SFC_PEANO = 1, AFF_SFC_HILBERT = 2 };
+
+typedef struct aff_sfc_curve_args {
+    const float *pos; int64_t p_sb, p_sn;
+    int B, N, curve, w, levels, first_w;
+    float cur_h[AFF_SFC_MAX_LEVELS];
+    float inv_h[AFF_SFC_MAX_LEVELS];
+    float level_scale[AFF_SFC_MAX_LEVELS];
+    float *keys;
+} aff_sfc_curve_args;
+
+typedef struct aff_sfc_anchor_args {
+    const float *pos; int64_t p_sb, p_sn;
+    int B, N;
+    float plw, plh;
+    int npw, ncell;
+    const int *cell_rank;
+    const float *prev_c;
+    const float *next_c;
+    float *keys;
+} aff_sfc_anchor_args;
+
+aff_status aff_sfc_curve_keys(const aff_sfc_curve_args *args, aff_stream_t stream);
+size_t aff_sfc_anchor_workspace_bytes(int B, int N);
+aff_status aff_sfc_anchor_keys(const aff_sfc_anchor_args *args, void *ws, size_t ws_bytes, aff_stream_t stream);
+size_t aff_sfc_argsort_workspace_bytes(int B, int N);
+aff_status aff_sfc_argsort(const float *keys, int B, int N, int64_t *ranking, void *ws, size_t ws_bytes,
+                           aff_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -43,7 +43,8 @@ def test_abi_version(lib):
 
 
 @pytest.mark.parametrize("cname,cls", [("aff_nbhd_attn_args", "NbhdAttnArgs"), ("aff_nbhd_attn_bwd_args", "NbhdAttnBwdArgs"),
-                                       ("aff_deform_args", "DeformArgs"), ("aff_deform_bwd_args", "DeformBwdArgs")])
+                                       ("aff_deform_args", "DeformArgs"), ("aff_deform_bwd_args", "DeformBwdArgs"),
+                                       ("aff_sfc_curve_args", "SfcCurveArgs"), ("aff_sfc_anchor_args", "SfcAnchorArgs")])
 def test_struct_layout_matches_header(tmp_path, cname, cls):
     """Size and every field offset of the ctypes mirror equal the C struct's (gcc on the header)."""
     struct = getattr(_lib, cls)

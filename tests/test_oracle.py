@@ -580,3 +580,70 @@ def test_deform_backward_oracle_catches_a_planted_sign_error(monkeypatch):
     scale = float(lg.grad.abs().max())
     assert float((ref["d_loc"] - lg.grad).abs().max()) <= 1e-6 * scale
     assert float((-ref["d_loc"] - lg.grad).abs().max()) > 1e-2 * scale
+
+
+def _walk_ok(keys, xs, ys):
+    """Sorted by key, the cells form a permutation walked in unit 4-neighbour steps."""
+    order = np.argsort(keys, kind="stable")
+    assert len(np.unique(keys)) == len(keys)
+    steps = np.abs(np.diff(xs[order])) + np.abs(np.diff(ys[order]))
+    return bool((steps == 1).all())
+
+
+@pytest.mark.parametrize("curve,h,w", [("peano", 9, 9), ("peano", 27, 27), ("peano", 3, 6), ("peano", 9, 18),
+                                       ("hilbert", 4, 4), ("hilbert", 8, 8), ("hilbert", 16, 16)])
+def test_sfc_oracle_curves_are_continuous_walks(curve, h, w):
+    """Peano at every depth; Hilbert to three levels.  The reference tracks the
+    Hilbert orientation as a rotation taken mod 3 (geometry.py:429-440), which
+    reproduces the curve to 8 x 8; a 16 x 16 grid is still a permutation but
+    takes exactly 8 jumps, which the restatement keeps."""
+    import torch
+    from oracle import sfc
+    ys, xs = np.meshgrid(np.arange(h), np.arange(w), indexing="ij")
+    pos = torch.from_numpy(np.stack([xs, ys], -1).reshape(1, -1, 2).astype(np.float32))
+    keys = (sfc.peano_keys if curve == "peano" else sfc.hilbert_keys)(h, w, pos)[0].numpy()
+    if curve == "hilbert" and h > 8:
+        order = np.argsort(keys)
+        steps = np.abs(np.diff(xs.reshape(-1)[order])) + np.abs(np.diff(ys.reshape(-1)[order]))
+        assert len(np.unique(keys)) == h * w and int((steps > 1).sum()) == 8
+        return
+    assert _walk_ok(keys, xs.reshape(-1), ys.reshape(-1))
+
+
+def test_sfc_oracle_known_orders():
+    import torch
+    from oracle import sfc
+
+    def order_of(fn, h, w):
+        ys, xs = np.meshgrid(np.arange(h), np.arange(w), indexing="ij")
+        pos = torch.from_numpy(np.stack([xs, ys], -1).reshape(1, -1, 2).astype(np.float32))
+        k = fn(h, w, pos)[0].numpy()
+        return [(int(xs.reshape(-1)[i]), int(ys.reshape(-1)[i])) for i in np.argsort(k)]
+
+    # first-order Peano: up the first column (from y = 2), down the second, up the third
+    assert order_of(sfc.peano_keys, 3, 3) == [(0, 2), (0, 1), (0, 0), (1, 0), (1, 1), (1, 2), (2, 2), (2, 1), (2, 0)]
+    # first-order Hilbert: the U (0,0) (0,1) (1,1) (1,0)
+    assert order_of(sfc.hilbert_keys, 2, 2) == [(0, 0), (0, 1), (1, 1), (1, 0)]
+    # second order Hilbert starts and ends on the bottom edge's corners of the U
+    o = order_of(sfc.hilbert_keys, 4, 4)
+    assert o[0] == (0, 0) and o[-1] == (3, 0) and len(set(o)) == 16
+    # the wide first Peano level continues the snake into the second 3 x 3 block
+    o = order_of(sfc.peano_keys, 3, 6)
+    assert o[:9] == [(0, 2), (0, 1), (0, 0), (1, 0), (1, 1), (1, 2), (2, 2), (2, 1), (2, 0)]
+    assert o[9] == (3, 0) and o[-1] == (5, 2)
+
+
+def test_sfc_oracle_scanline_matches_product_cpu_path():
+    """The oracle's scanline anchor key and the product's CPU ordering (two writes of
+    geometry.py:199-268) rank jittered tokens identically."""
+    import torch
+    from oracle import sfc
+    from affmae_amd.utils.geometry import space_filling_cluster
+    g = torch.Generator().manual_seed(3)
+    side = 40
+    cells = torch.randperm(side * side, generator=g)[:900]
+    pos = torch.stack([cells % side, cells // side], -1).float().unsqueeze(0)
+    pos = pos + torch.rand(pos.shape, generator=g) * 0.9
+    rank_prod = space_filling_cluster(pos, 8, side, side)[4][0, :, 0]
+    key = sfc.anchor_keys(pos, 8, side, side)
+    assert torch.equal(rank_prod, key[0].sort(stable=True)[1])
