@@ -147,6 +147,7 @@ SIGNATURES = {
     "aff_nbhd_attn_workspace_bytes": (SZ, [ctypes.POINTER(NbhdAttnArgs)]),
     "aff_nbhd_attn_fwd": (I32, [ctypes.POINTER(NbhdAttnArgs), P]),
     "aff_nbhd_attn_path": (I32, [ctypes.POINTER(NbhdAttnArgs)]),
+    "aff_nbhd_attn_proj_fwd": (I32, [ctypes.POINTER(NbhdAttnArgs), P, P, P]),
     "aff_nbhd_attn_bwd_workspace_bytes": (SZ, [ctypes.POINTER(NbhdAttnBwdArgs)]),
     "aff_nbhd_attn_bwd": (I32, [ctypes.POINTER(NbhdAttnBwdArgs), P]),
     "aff_weighted_features_fwd": (I32, [P, I32, I64, I64, I64, I64, P, I32, I64, I64, P, I32, I64, I64,

@@ -307,10 +307,12 @@ __device__ __forceinline__ void tile_rows(const aff_nbhd_attn_args &a, int b, in
 // its k index in the order the S result lays slots out in the lanes, and
 // V^T is read in that same order from the chunk's V rows in LDS by
 // ds_read_b64_tr_b16.  K and V rows are fetched one chunk ahead.
-template <typename T, bool BLANK>
+// STAGE: the normalised outputs of the lane (channels 8 j + 4 hh + i of query ql at
+// yo[4 j + i]) stay in registers for the projection epilogue instead of going to out.
+template <typename T, bool BLANK, bool STAGE = false>
 __device__ __forceinline__ void wave_head_one(const aff_nbhd_attn_args &a, int b, int n0, int U, const int *ulist,
                                               const uint16_t *pw, const float *bm, float nm, uint16_t *vbuf, int h,
-                                              int hbase) {
+                                              int hbase, float *yo = nullptr) {
     using namespace wt;
     using MM = Mfma32<T>;
     const int lane = threadIdx.x & 63;
@@ -473,7 +475,24 @@ __device__ __forceinline__ void wave_head_one(const aff_nbhd_attn_args &a, int b
         const float pbl = BLANK ? __builtin_amdgcn_exp2f(sb - m) : 0.f;
         const float l = pair_sum(lp) + pbl + (nm > 0.f ? nm * __builtin_amdgcn_exp2f(MASKED_LOGIT * LOG2E - m) : 0.f);
         const float inv = __builtin_amdgcn_rcpf(l + 1e-12f);  // 1 ulp: outputs are 16-bit
-        if (qout) {
+        if constexpr (STAGE) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int d0 = 8 * j + 4 * hh;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float y = O[4 * j + i];
+                    if constexpr (BLANK) {
+                        const uint16_t bv = *reinterpret_cast<const uint16_t *>(
+                            static_cast<const char *>(a.blank_v) + (h * HD + d0 + i) * 2);
+                        y += pbl * MM::to_f32(bv);
+                    }
+                    yo[4 * j + i] = y * inv;
+                }
+            }
+            if (qout && a.lse && hh == 0)
+                a.lse[((int64_t)b * H + h) * N + n0 + ql] = m * 0.6931471805599453f + __logf(l + 1e-12f);
+        } else if (qout) {
             T *orow = static_cast<T *>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)(n0 + ql) * a.o_sn;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -504,8 +523,52 @@ __device__ __forceinline__ void wave_heads(const aff_nbhd_attn_args &a, int b, i
     for (int h = h0; h < hend; h += hstep) wave_head_one<T, BLANK>(a, b, n0, U, ulist, pw, bm, nm, vbuf, h, hbase);
 }
 
-template <typename T, int BIAS, bool IDX64, bool BLANK>
-__global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nbhd_attn_args a, int HG) {
+// The output projection fused into the wave kernel's epilogue (ClusterAttention's
+// proj, reference attention.py:204-205): y = O W^T + b for the tile's 32 queries,
+// with every head of the image in the workgroup (at most NW heads, one per wave).
+struct ProjArgs {
+    const void *w;   // [C, C] 16-bit (the attention dtype), row o = output channel o
+    const float *b;  // [C] or NULL
+};
+
+// y^T (32 output channels x 32 queries) per MFMA block = W_block O^T; O is the
+// tile's [32][C] 16-bit block in LDS (row pitch op), W rows from global memory.
+template <typename T>
+__device__ __forceinline__ void proj_epilogue(const aff_nbhd_attn_args &a, const ProjArgs &pj, int b, int n0,
+                                              const uint16_t *otile, int op, int C) {
+    using namespace wt;
+    using MM = Mfma32<T>;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int hh = lane >> 5, ql = lane & 31;
+    const int nblk = C / 32;
+    for (int ob = w; ob < nblk; ob += NW) {
+        f32x16 Y;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) Y[r] = 0.f;
+        const uint16_t *wrow = static_cast<const uint16_t *>(pj.w) + (int64_t)(32 * ob + ql) * C + 8 * hh;
+        const uint16_t *orow = otile + ql * op + 8 * hh;
+        for (int k0 = 0; k0 < C; k0 += 16) {
+            const uint4 wa = *reinterpret_cast<const uint4 *>(wrow + k0);
+            const uint4 ov = *reinterpret_cast<const uint4 *>(orow + k0);
+            Y = MM::mma(wa, ov, Y);
+        }
+        if (n0 + ql < a.N) {
+            T *yrow = static_cast<T *>(a.out) + (int64_t)b * a.o_sb + (int64_t)(n0 + ql) * a.o_sn + 32 * ob;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int o0 = 8 * j + 4 * hh;
+                float y[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) y[i] = Y[4 * j + i] + (pj.b ? pj.b[32 * ob + o0 + i] : 0.f);
+                *reinterpret_cast<uint2 *>(yrow + o0) = make_uint2(MM::pack2(y[0], y[1]), MM::pack2(y[2], y[3]));
+            }
+        }
+    }
+}
+
+template <typename T, int BIAS, bool IDX64, bool BLANK, bool PROJ = false>
+__global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nbhd_attn_args a, int HG,
+                                                                    const ProjArgs pj) {
     using namespace wt;
     using MM = Mfma32<T>;
     // pw[q][slot]: byte offset in bm of the (query, neighbour) pair's biases; 0 (the
@@ -780,13 +843,50 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
         fallback = red[1] != 0;
     }
 
-    if (fallback) {
-        tile_rows<T, BIAS>(a, b, n0, TQ, hb, hn);
-        return;
+    if constexpr (!PROJ) {
+        if (fallback) {
+            tile_rows<T, BIAS>(a, b, n0, TQ, hb, hn);
+            return;
+        }
+        // ---- head phase: wave w, heads hb + w, hb + w + NW, ... of the group
+        wave_heads<T, BLANK>(a, b, n0, U, ulist, pw, bm, nmq_s[lane & 31], sh.vb[w], hb + w, NW, hb + hn, hb);
+    } else {
+        // every head of the image in this workgroup, at most one per wave (host-checked);
+        // the [32][C] output block is staged in bm's space once every wave is past it
+        const int C = H * HD, op = C + 8;
+        uint16_t *otile = reinterpret_cast<uint16_t *>(bm);
+        if (fallback) {
+            // the per-row routine writes the tile's rows to out; they come back as the block
+            tile_rows<T, BIAS>(a, b, n0, TQ, 0, H);
+            __syncthreads();
+            for (int e = t; e < TQ * (C / 8); e += THREADS) {
+                const int qq = e / (C / 8), c8 = 8 * (e % (C / 8));
+                uint4 v = make_uint4(0, 0, 0, 0);
+                if (n0 + qq < N)
+                    v = *reinterpret_cast<const uint4 *>(static_cast<const T *>(a.out) + (int64_t)b * a.o_sb +
+                                                         (int64_t)(n0 + qq) * a.o_sn + c8);
+                *reinterpret_cast<uint4 *>(otile + qq * op + c8) = v;
+            }
+            __syncthreads();
+        } else {
+            float yo[16];
+            const bool has = w < H;
+            if (has)
+                wave_head_one<T, BLANK, true>(a, b, n0, U, ulist, pw, bm, nmq_s[lane & 31], sh.vb[w], w, 0, yo);
+            __syncthreads();
+            if (has) {
+                const int hh = lane >> 5, ql = lane & 31;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int c0 = w * HD + 8 * j + 4 * hh;
+                    *reinterpret_cast<uint2 *>(otile + ql * op + c0) =
+                        make_uint2(MM::pack2(yo[4 * j], yo[4 * j + 1]), MM::pack2(yo[4 * j + 2], yo[4 * j + 3]));
+                }
+            }
+            __syncthreads();
+        }
+        proj_epilogue<T>(a, pj, b, n0, otile, op, C);
     }
-
-    // ---- head phase: wave w, heads hb + w, hb + w + NW, ... of the group
-    wave_heads<T, BLANK>(a, b, n0, U, ulist, pw, bm, nmq_s[lane & 31], sh.vb[w], hb + w, NW, hb + hn, hb);
 }
 
 using KernelFn = void (*)(const aff_nbhd_attn_args);
@@ -847,23 +947,24 @@ inline int wave_heads_per_group(const aff_nbhd_attn_args &a) {
     return a.H < hg ? a.H : hg;
 }
 
-using WaveFn = void (*)(const aff_nbhd_attn_args, int);
+using WaveFn = void (*)(const aff_nbhd_attn_args, int, const ProjArgs);
 
-template <typename T, int BIAS>
+template <typename T, int BIAS, bool PROJ>
 WaveFn pick_wave3(bool i64, bool blank) {
-    if (i64) return blank ? nbhd_attn_wave_kernel<T, BIAS, true, true> : nbhd_attn_wave_kernel<T, BIAS, true, false>;
-    return blank ? nbhd_attn_wave_kernel<T, BIAS, false, true> : nbhd_attn_wave_kernel<T, BIAS, false, false>;
+    if (i64)
+        return blank ? nbhd_attn_wave_kernel<T, BIAS, true, true, PROJ> : nbhd_attn_wave_kernel<T, BIAS, true, false, PROJ>;
+    return blank ? nbhd_attn_wave_kernel<T, BIAS, false, true, PROJ> : nbhd_attn_wave_kernel<T, BIAS, false, false, PROJ>;
 }
 
-template <typename T>
+template <typename T, bool PROJ = false>
 WaveFn pick_wave(const aff_nbhd_attn_args &a) {
     const bool i64 = a.idx_is_i64 != 0, blank = a.blank_k != nullptr;
     switch (a.bias_mode) {
-        case 0: return pick_wave3<T, 0>(i64, blank);
-        case 1: return pick_wave3<T, 1>(i64, blank);
-        case 2: return pick_wave3<T, 2>(i64, blank);
-        case 3: return pick_wave3<T, 3>(i64, blank);
-        default: return pick_wave3<T, 4>(i64, blank);
+        case 0: return pick_wave3<T, 0, PROJ>(i64, blank);
+        case 1: return pick_wave3<T, 1, PROJ>(i64, blank);
+        case 2: return pick_wave3<T, 2, PROJ>(i64, blank);
+        case 3: return pick_wave3<T, 3, PROJ>(i64, blank);
+        default: return pick_wave3<T, 4, PROJ>(i64, blank);
     }
 }
 
@@ -928,7 +1029,7 @@ extern "C" aff_status aff_nbhd_attn_fwd(const aff_nbhd_attn_args *args, aff_stre
         const int64_t blocks = ntiles * ((a.H + hg - 1) / hg);
         AFF_CHECK_ARG(blocks < (int64_t)1 << 31, "aff_nbhd_attn_fwd: problem too large");
         const attn::WaveFn fn = a.dtype == AFF_BF16 ? attn::pick_wave<bf16_t>(a) : attn::pick_wave<f16_t>(a);
-        hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(attn::THREADS), 0, hs, a, hg);
+        hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(attn::THREADS), 0, hs, a, hg, attn::ProjArgs{nullptr, nullptr});
         return check_launch("aff_nbhd_attn_fwd (wave tiles)");
     }
     attn::KernelFn fn = nullptr;
@@ -941,4 +1042,38 @@ extern "C" aff_status aff_nbhd_attn_fwd(const aff_nbhd_attn_args *args, aff_stre
     AFF_CHECK_ARG(blocks < (int64_t)1 << 31, "aff_nbhd_attn_fwd: problem too large");
     hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(attn::THREADS), 0, hs, a);
     return check_launch("aff_nbhd_attn_fwd");
+}
+
+extern "C" aff_status aff_nbhd_attn_proj_fwd(const aff_nbhd_attn_args *args, const void *proj_w, const float *proj_b,
+                                             aff_stream_t stream) {
+    AFF_CHECK_ARG(args != nullptr, "aff_nbhd_attn_proj_fwd: NULL args");
+    const aff_nbhd_attn_args &a = *args;
+    if (!(a.dtype == AFF_BF16 || a.dtype == AFF_F16) || a.D != attn::wt::HD || !attn::use_wave_path(a) ||
+        a.H > attn::wt::NW || attn::wave_heads_per_group(a) < a.H)
+        return fail(AFF_ERR_UNSUPPORTED,
+                    "aff_nbhd_attn_proj_fwd: needs 16-bit q/k/v, head_dim 32, at most %d heads and M <= %d (H=%d M=%d D=%d)",
+                    attn::wt::NW, attn::wt::MAXHM / (a.H > 0 ? a.H : 1), a.H, a.M, a.D);
+    AFF_CHECK_ARG(proj_w && attn::aligned16(proj_w), "aff_nbhd_attn_proj_fwd: proj_w NULL or not 16-byte aligned");
+    AFF_CHECK_ARG(a.o_sh == a.D && a.o_sn >= (int64_t)a.H * a.D,
+                  "aff_nbhd_attn_proj_fwd: out must be [B, N, H * D] rows (o_sh = D)");
+    AFF_CHECK_ARG(a.B >= 0 && a.N >= 0 && a.M >= 0, "aff_nbhd_attn_proj_fwd: bad sizes");
+    if ((int64_t)a.B * a.N == 0) return AFF_OK;
+    AFF_CHECK_ARG(a.q && a.k && a.v && a.out && (a.M == 0 || a.member_idx), "aff_nbhd_attn_proj_fwd: NULL pointer");
+    AFF_CHECK_ARG((a.blank_k == nullptr) == (a.blank_v == nullptr), "aff_nbhd_attn_proj_fwd: blank_k / blank_v");
+    const int64_t st16[] = {a.q_sb, a.q_sh, a.q_sn, a.k_sb, a.k_sh, a.k_sn, a.v_sb, a.v_sh, a.v_sn, a.o_sb, a.o_sn};
+    for (int64_t s : st16) AFF_CHECK_ARG((s * 2) % 16 == 0, "aff_nbhd_attn_proj_fwd: strides must keep 16-byte rows");
+    AFF_CHECK_ARG(attn::aligned16(a.q) && attn::aligned16(a.k) && attn::aligned16(a.v) && attn::aligned16(a.out),
+                  "aff_nbhd_attn_proj_fwd: q/k/v/out must be 16-byte aligned");
+    AFF_CHECK_ARG(a.bias_mode >= 0 && a.bias_mode <= 4, "aff_nbhd_attn_proj_fwd: bias_mode %d", a.bias_mode);
+    if (a.bias_mode == 1) AFF_CHECK_ARG(a.bias, "aff_nbhd_attn_proj_fwd: bias_mode 1 needs bias");
+    if (a.bias_mode == 2) AFF_CHECK_ARG(a.pe_idx && a.table, "aff_nbhd_attn_proj_fwd: bias_mode 2 needs pe_idx, table");
+    if (a.bias_mode == 3) AFF_CHECK_ARG(a.pos && a.pos_w && a.pos_b, "aff_nbhd_attn_proj_fwd: bias_mode 3 inputs");
+    if (a.bias_mode == 4)
+        AFF_CHECK_ARG(a.pos && a.table && a.rel_width >= 1 && a.rel_width < 32768, "aff_nbhd_attn_proj_fwd: mode 4");
+    const int64_t blocks = attn::tile_count(a);
+    AFF_CHECK_ARG(blocks < (int64_t)1 << 31, "aff_nbhd_attn_proj_fwd: problem too large");
+    const attn::WaveFn fn = a.dtype == AFF_BF16 ? attn::pick_wave<bf16_t, true>(a) : attn::pick_wave<f16_t, true>(a);
+    hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(attn::THREADS), 0, static_cast<hipStream_t>(stream), a, a.H,
+                       attn::ProjArgs{proj_w, proj_b});
+    return check_launch("aff_nbhd_attn_proj_fwd");
 }

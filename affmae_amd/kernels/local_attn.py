@@ -214,6 +214,40 @@ def nbhd_attn_fwd(q, k, v, member_idx, scale, *, bias=None, pe_idx=None, pe_tabl
     return out, lse
 
 
+def nbhd_attn_proj_fwd(q, k, v, member_idx, scale, proj_w, proj_b=None, *, pe_idx=None, pe_table=None, pos=None,
+                       rel_width=REL_POS_WIDTH, mask=None, blank_k=None, blank_v=None, out=None):
+    """Attention with the output projection fused (aff_nbhd_attn_proj_fwd):
+    [B,N,H*D] = concat_h attention(q, k, v)[:, h] @ proj_w^T + proj_b.
+
+    q, k, v as for nbhd_attn_fwd; proj_w [H*D, H*D] (cast to q's dtype),
+    proj_b [H*D] or None.  Returns None when the shape is outside the fused
+    kernel's case (16-bit, head_dim 32, H <= 4, H*M <= 192), so the caller
+    runs the two steps instead."""
+    lib = _lib.load()
+    B, H, N, D = q.shape
+    C = H * D
+    if q.dtype not in (torch.bfloat16, torch.float16) or D != 32 or H > 4 or tuple(proj_w.shape) != (C, C):
+        return None
+    a, keep, dev = _attn_args(q, k, v, member_idx, scale, pe_idx=pe_idx, pe_table=pe_table, pos=pos,
+                              rel_width=rel_width, mask=mask, blank_k=blank_k, blank_v=blank_v)
+    if out is None:
+        out = torch.empty((B, N, C), dtype=q.dtype, device=dev)
+    assert tuple(out.shape) == (B, N, C) and out.dtype == q.dtype and out.stride(-1) == 1 and out.stride(1) == C
+    w = proj_w.detach().to(q.dtype).contiguous()
+    bias = proj_b.detach().to(torch.float32).contiguous() if proj_b is not None else None
+    keep += [out, w] + ([bias] if bias is not None else [])
+    a.out, a.o_sb, a.o_sh, a.o_sn = out.data_ptr(), out.stride(0), D, C
+    st = lib.aff_nbhd_attn_proj_fwd(ctypes.byref(a), w.data_ptr(), bias.data_ptr() if bias is not None else None,
+                                    _lib.stream_ptr(dev))
+    if st == _lib.AFF_ERR_UNSUPPORTED:
+        return None
+    _lib.check(st, "aff_nbhd_attn_proj_fwd")
+    if _path_log is not None:
+        _path_log.append("wave+proj")
+    del keep
+    return out
+
+
 def nbhd_attn_bwd(dout, q, k, v, member_idx, scale, out, lse, *, bias=None, pe_idx=None, pe_table=None, pos=None,
                   rel_width=REL_POS_WIDTH, mask=None, blank_k=None, blank_v=None, dq=None, dk=None, dv=None,
                   want_dbias=False, want_dtable=False):

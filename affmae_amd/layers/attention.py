@@ -28,7 +28,7 @@ from ..kernels.fused_deform_attn import (
     fused_knn_deformable_self_attention,
 )
 from ..kernels.knn import knn as hip_knn
-from ..kernels.local_attn import ClusterAttnFunction
+from ..kernels.local_attn import nbhd_attn_proj_fwd, ClusterAttnFunction
 from ..kernels.msdetrpc import MSDETRPCFunction
 from ..utils.pos_embed import pre_table_fp16, pre_table_fp32
 
@@ -111,10 +111,29 @@ class ClusterAttention(nn.Module):
         if cluster_mask is not None:
             mask = (cluster_mask > 0) if cluster_mask.dtype != torch.bool else cluster_mask
             mask = mask.unsqueeze(1)                                  # broadcast over heads
+        if self._fuse_proj(q, kv):
+            # inference: the projection runs in the attention kernel's epilogue
+            qh = q.view(B, N, H, Ch).permute(0, 2, 1, 3)
+            kvh = kv.view(B, N, H, 2 * Ch).permute(0, 2, 1, 3)
+            y = nbhd_attn_proj_fwd(qh, kvh[..., :Ch], kvh[..., Ch:], member_idx, self.scale, self.proj.weight,
+                                   self.proj.bias, pe_idx=pe_idx, pe_table=self.pe_table(dtype), mask=mask,
+                                   blank_k=self.blank_k.view(H, Ch).to(dtype), blank_v=self.blank_v.view(H, Ch).to(dtype))
+            if y is not None:
+                return y
         out = ClusterAttnFunction.apply(q, kv, member_idx, pe_idx, self.pe_table(dtype), mask,
                                         self.blank_k.view(H, Ch), self.blank_v.view(H, Ch), self.scale, H)
         out = self.proj(out)
         return self.proj_drop(out)
+
+    def _fuse_proj(self, q, kv):
+        """The fused projection serves forwards that record no gradients, with the
+        projection's dropout inactive."""
+        if not q.is_cuda or (self.proj_drop.p > 0 and self.training):
+            return False
+        if torch.is_grad_enabled() and (q.requires_grad or kv.requires_grad
+                                        or any(p.requires_grad for p in self.parameters())):
+            return False
+        return True
 
     def _global(self, feat, q, kv, pe_idx):
         """Dense attention with bias and blank token (attention.py:157-180), torch SDPA."""

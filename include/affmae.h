@@ -168,6 +168,27 @@ aff_status aff_nbhd_attn_fwd(const aff_nbhd_attn_args *args, aff_stream_t stream
 enum { AFF_ATTN_PATH_ROW = 0, AFF_ATTN_PATH_WAVE = 2 };
 int aff_nbhd_attn_path(const aff_nbhd_attn_args *args);
 
+
+/* ------------------------------------------------------------------------ *
+ * Neighbourhood attention with ClusterAttention's output projection fused.
+ *
+ * Replaces: the attention (as aff_nbhd_attn_fwd) followed by
+ *           out = self.proj(out)   src/layers/attention.py:204-205
+ *
+ * args as for aff_nbhd_attn_fwd, except that args->out receives the
+ * projected rows y[b, n, :] = O[b, n, :] proj_w^T + proj_b, with O[b, n, :]
+ * the attention output of all heads concatenated ([B, N, H * D], o_sh = D,
+ * o_sn >= H * D).  proj_w: [H*D, H*D] in the attention dtype, row o = output
+ * channel o (nn.Linear's weight), 16-byte aligned; proj_b: fp32 [H*D] or NULL.
+ * The attention output is rounded to the attention dtype before the
+ * projection, as the two-step composition does.  Only the wave kernel's
+ * case with every head in one workgroup is fused: 16-bit q/k/v, head_dim 32,
+ * H <= 4 and H * M <= 192; other shapes return AFF_ERR_UNSUPPORTED (the
+ * caller then runs aff_nbhd_attn_fwd and its own projection).  lse is
+ * written when args->lse is set.
+ * ------------------------------------------------------------------------ */
+aff_status aff_nbhd_attn_proj_fwd(const aff_nbhd_attn_args *args, const void *proj_w, const float *proj_b,
+                                  aff_stream_t stream);
 /* ------------------------------------------------------------------------ *
  * Neighbourhood (cluster) flash attention, backward.
  *
