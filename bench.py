@@ -140,6 +140,7 @@ def cfg5_encoder(dev, reps: int):
     import torch
     from affmae_amd import workloads
     from affmae_amd.layers import aff as aff_mod
+    from affmae_amd.layers import attention as attn_mod
     from affmae_amd.kernels import local_attn
 
     enc = workloads.cfg5_encoder().to(dev).eval()
@@ -156,7 +157,7 @@ def cfg5_encoder(dev, reps: int):
     # one forward with the hot-path entry points wrapped to record their arguments
     calls = []
     stage = {"i": -1}
-    orig = (aff_mod.knn, aff_mod.weighted_features, local_attn.nbhd_attn_fwd)
+    orig = (aff_mod.knn, aff_mod.weighted_features, local_attn.nbhd_attn_fwd, attn_mod.nbhd_attn_proj_fwd)
 
     def rec_knn(q, r, k, *a, **kw):
         stage["i"] += 1
@@ -171,11 +172,19 @@ def cfg5_encoder(dev, reps: int):
         calls.append(("attn", stage["i"], (a, kw)))
         return orig[2](*a, **kw)
 
+    def rec_proj(*a, **kw):
+        y = orig[3](*a, **kw)
+        if y is not None:                         # the attention ran with its projection fused
+            calls.append(("attn_proj", stage["i"], (a, kw)))
+        return y
+
     aff_mod.knn, aff_mod.weighted_features, local_attn.nbhd_attn_fwd = rec_knn, rec_wf, rec_attn
+    attn_mod.nbhd_attn_proj_fwd = rec_proj
     try:
         fwd()
     finally:
-        aff_mod.knn, aff_mod.weighted_features, local_attn.nbhd_attn_fwd = orig
+        aff_mod.knn, aff_mod.weighted_features, local_attn.nbhd_attn_fwd = orig[:3]
+        attn_mod.nbhd_attn_proj_fwd = orig[3]
     torch.cuda.synchronize()
 
     el = lambda t: t.numel() * t.element_size()
@@ -196,10 +205,15 @@ def cfg5_encoder(dev, reps: int):
             st["merge_bytes"] += el(wts) + el(idx) + el(feat) + B5 * n2 * IC * feat.shape[-1] * feat.element_size()
         else:
             a, kw = args
-            t = time_events(lambda: orig[2](*a, **kw), reps)
+            fused = kind == "attn_proj"
+            t = time_events(lambda: (orig[3] if fused else orig[2])(*a, **kw), reps)
             q, kk, v, mi = a[0], a[1], a[2], a[3]
             mask, table, pe = kw.get("mask"), kw.get("pe_table"), kw.get("pe_idx")
+            # q, k, v in, one [B, N, H*D] output (the projected rows when fused, plus the weight)
             by = 4 * el(q) + el(mi) + (el(pe) if pe is not None else 0) + (el(table) if table is not None else 0)
+            if fused:
+                by += a[5].numel() * q.element_size()
+                st["proj_fused"] = True
             if mask is not None:
                 by += mask.numel()                        # read as uint8
             st["attn_ms"] += t
@@ -210,6 +224,7 @@ def cfg5_encoder(dev, reps: int):
            "hot_path_ms": sum(s_["attn_ms"] + s_["knn_ms"] + s_["merge_ms"] for s_ in stages), "stages": []}
     for i, st in enumerate(stages):
         e = {"tokens": st["n"], "heads": st.get("heads"), "attn_calls": st["attn_calls"],
+             "attn_proj_fused": bool(st.get("proj_fused", False)),
              "attn_ms": st["attn_ms"], "knn_ms": st["knn_ms"], "merge_ms": st["merge_ms"]}
         if st["attn_ms"] > 0:
             e["attn_hbm_frac"] = st["attn_bytes"] / (st["attn_ms"] * 1e-3) / HBM_PEAK
