@@ -90,6 +90,84 @@ __global__ __launch_bounds__(THREADS) void wfeat_vec_kernel(const WFArgs a) {
     }
 }
 
+// IC = 4 with each row's weights packed [M][4] (the merge's layout): the four
+// weights of a neighbour come as one vector load, and the next group's indices
+// are loaded while the current group's rows are in flight.
+template <typename TW>
+__device__ __forceinline__ void load_w4(const TW *p, float (&o)[4]) {
+    if constexpr (sizeof(TW) == 4) {
+        const float4 v = *reinterpret_cast<const float4 *>(p);
+        o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+    } else {
+        const uint2 v = *reinterpret_cast<const uint2 *>(p);
+        const uint16_t h[4] = {uint16_t(v.x & 0xffffu), uint16_t(v.x >> 16), uint16_t(v.y & 0xffffu), uint16_t(v.y >> 16)};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if constexpr (__is_same(TW, bf16_t)) o[i] = bf16_to_f32(h[i]);
+            else o[i] = float(__builtin_bit_cast(_Float16, h[i]));
+        }
+    }
+}
+
+template <typename T, typename TW, bool IDX64, int LPR>
+__global__ __launch_bounds__(THREADS) void wfeat4_kernel(const WFArgs a) {
+    using IO = ElemIO<T>;
+    constexpr int ROWS = THREADS / LPR;
+    const uint32_t bid = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int sub = threadIdx.x % LPR;
+    const int64_t row = (int64_t)bid * ROWS + threadIdx.x / LPR;
+    if (row >= (int64_t)a.B * a.Nout) return;
+    const int i = int(row % a.Nout), b = int(row / a.Nout);
+    const T *F = static_cast<const T *>(a.f) + (int64_t)b * a.f_sb;
+    const int64_t ibase = (int64_t)b * a.i_sb + (int64_t)i * a.i_sn;
+    const TW *W = static_cast<const TW *>(a.w) + (int64_t)b * a.w_sb + (int64_t)i * a.w_sn;
+    T *O = static_cast<T *>(a.out) + (int64_t)b * a.o_sb + (int64_t)i * a.o_sn;
+    auto index = [&](int m) -> int {
+        if (m >= a.M) return -1;
+        const int64_t v = IDX64 ? static_cast<const int64_t *>(a.idx)[ibase + m]
+                                : int64_t(static_cast<const int32_t *>(a.idx)[ibase + m]);
+        return (v >= 0 && v < a.Nsrc) ? int(v) : -1;
+    };
+    for (int c0 = sub * 8; c0 < a.C; c0 += LPR * 8) {
+        float acc[4][8];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[t][e] = 0.f;
+        int id[NB];
+#pragma unroll
+        for (int u = 0; u < NB; ++u) id[u] = index(u);
+        for (int m0 = 0; m0 < a.M; m0 += NB) {
+            typename IO::raw8 fr[NB];
+#pragma unroll
+            for (int u = 0; u < NB; ++u) fr[u] = IO::load_raw(F + (int64_t)(id[u] >= 0 ? id[u] : 0) * a.f_sn + c0);
+            float wv[NB][4];
+#pragma unroll
+            for (int u = 0; u < NB; ++u) {
+                if (m0 + u < a.M) load_w4(W + (int64_t)(m0 + u) * 4, wv[u]);
+                else wv[u][0] = wv[u][1] = wv[u][2] = wv[u][3] = 0.f;
+            }
+            int idn[NB];
+#pragma unroll
+            for (int u = 0; u < NB; ++u) idn[u] = index(m0 + NB + u);
+#pragma unroll
+            for (int u = 0; u < NB; ++u) {
+                if (id[u] < 0) continue;
+                float fv[8];
+                IO::cvt(fr[u], fv);
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc[t][e] += wv[u][t] * fv[e];
+            }
+#pragma unroll
+            for (int u = 0; u < NB; ++u) id[u] = idn[u];
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) IO::store8(O + (int64_t)t * a.o_sic + c0, acc[t]);
+    }
+}
+
 // Scalar path for any C / alignment: one lane per (row, channel).
 template <typename T>
 __global__ __launch_bounds__(THREADS) void wfeat_scalar_kernel(const WFArgs a) {
@@ -252,7 +330,27 @@ inline int lanes_for(int C) {
 template <typename T>
 aff_status launch_wfeat(const WFArgs &a, bool vec, hipStream_t s) {
     const int64_t rows = (int64_t)a.B * a.Nout;
-    if (vec) {
+    if (vec && a.IC == 4 && a.w_sic == 1 && a.w_sm == 4 &&
+        (reinterpret_cast<uintptr_t>(a.w) & (a.w_dtype == AFF_F32 ? 15 : 7)) == 0 &&
+        (a.w_sb * 4) % 16 == 0 && (a.w_sn * 4) % 16 == 0) {
+        const int lpr = lanes_for(a.C);
+        const int64_t blocks = (rows * lpr + THREADS - 1) / THREADS;
+        auto go = [&](auto tw) {
+            using TW = decltype(tw);
+            switch (lpr) {
+#define WF4_CASE(L)                                                                                             \
+    case L:                                                                                                     \
+        if (a.idx_i64) hipLaunchKernelGGL((wfeat4_kernel<T, TW, true, L>), dim3((unsigned)blocks), dim3(THREADS), 0, s, a); \
+        else hipLaunchKernelGGL((wfeat4_kernel<T, TW, false, L>), dim3((unsigned)blocks), dim3(THREADS), 0, s, a);         \
+        break;
+                WF4_CASE(1) WF4_CASE(2) WF4_CASE(4) WF4_CASE(8) WF4_CASE(16) WF4_CASE(32) WF4_CASE(64)
+#undef WF4_CASE
+            }
+        };
+        if (a.w_dtype == AFF_F32) go(float{});
+        else if (a.w_dtype == AFF_BF16) go(bf16_t{});
+        else go(f16_t{});
+    } else if (vec) {
         const int lpr = lanes_for(a.C);
         const int64_t blocks = (rows * lpr + THREADS - 1) / THREADS;
         switch (lpr) {
