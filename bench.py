@@ -12,8 +12,11 @@ over the whole batch with every input already resident in HBM.
 Prints one JSON line.  ``value`` is tokens/s through the whole step;
 ``roofline`` is for the attention kernel (the dominant one), with its
 average launch duration measured by HIP events on the launch stream inside
-the timed region; ``cpu_baseline`` times the CPU oracle (oracle/oracle.c,
-OpenMP) on a bounded sample of the same images on this host.
+the timed region; ``cpu_baseline`` times the reference's own PyTorch path in
+torch-CPU fp32 (oracle/torch_path.py) on the same images on this host.  The
+HBM traffic and SQ-counter figures come from the committed rocprofv3
+summaries under profiles/ and are null when the kernel source has changed
+since they were measured.
 """
 from __future__ import annotations
 
@@ -67,18 +70,27 @@ def cfg4_bytes(w) -> int:
             + B4 * Nq * H4 * C4 * w["values"].element_size())
 
 
-def measured_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE summary (lines "traffic: <kernel> <bytes>"), or None."""
-    f = ROOT / "profiles" / "hbm_traffic_fetch_write.md"
+def profile_figure(fname: str, tag: str, kernel: str, cast=float):
+    """A figure from a committed rocprofv3 summary under profiles/ (lines
+    "<tag>: <kernel> <value> <source>@<sha256 prefix>"), or None when there is no such line
+    or the kernel source has changed since it was measured (the figure is stale)."""
+    import hashlib
+    f = ROOT / "profiles" / fname
     try:
         for line in f.read_text().splitlines():
             parts = line.split()
-            if len(parts) == 3 and parts[0] == "traffic:" and parts[1] == kernel:
-                return int(parts[2])
+            if len(parts) == 4 and parts[0] == tag + ":" and parts[1] == kernel:
+                src, _, sha = parts[3].partition("@")
+                cur = hashlib.sha256((ROOT / src).read_bytes()).hexdigest()
+                return cast(parts[2]) if sha and cur.startswith(sha) else None
     except OSError:
         pass
     return None
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the FETCH_SIZE / WRITE_SIZE summary, or None."""
+    return profile_figure("hbm_traffic_fetch_write.md", "traffic", kernel, int)
 
 
 def time_events(fn, reps: int):
@@ -458,11 +470,15 @@ def main() -> int:
         },
         "knn": {"ms": knn_ms, "queries_per_s": B * N / (knn_ms * 1e-3),
                 "algorithmic_bytes": knn_bytes(),
-                "hbm_frac": knn_bytes() / (knn_ms * 1e-3) / HBM_PEAK},
+                "hbm_frac": knn_bytes() / (knn_ms * 1e-3) / HBM_PEAK,
+                "valu_busy": profile_figure("sq_counters_attn_knn_cfg2.md", "valu_busy", "knn")},
         "attention": {"ms": attn_ms, "tokens_per_s": B * N / (attn_ms * 1e-3),
-                      "raster_order_ms": attn_raster_ms},
+                      "raster_order_ms": attn_raster_ms,
+                      "valu_busy": profile_figure("sq_counters_attn_knn_cfg2.md", "valu_busy", "attn"),
+                      "mfma_busy": profile_figure("sq_counters_attn_knn_cfg2.md", "mfma_busy", "attn"),
+                      "lds_bank_conflict": profile_figure("sq_counters_attn_knn_cfg2.md", "lds_conflict", "attn")},
         "roofline": {
-            "kernel": "nbhd_attn_wave_kernel<bf16_t, 4, false, true>",
+            "kernel": "nbhd_attn_wave_kernel<bf16_t, 4, false, true, false>",
             "bound": "hbm",
             "achieved": achieved / 1e9,
             "peak": HBM_PEAK / 1e9,
