@@ -104,46 +104,58 @@ struct MapArgs {
     float eps;
 };
 
-// One lane per pixel; channels in registers.
-template <typename TI, typename TO>
+// One lane per pixel; channels in registers.  Grid: (pixel blocks of one image, B);
+// pixel offsets inside one image are 32-bit (host-checked), so the pixel's row,
+// column and token need only 32-bit divisions.  MC >= C channels are compiled in:
+// every channel load is unconditional (channels past C re-read channel C - 1 and
+// are dropped), so a lane's loads are all in flight together.
+template <typename TI, typename TO, int MC>
 __global__ __launch_bounds__(THREADS) void ln_map_kernel(MapArgs a) {
-    const int64_t HW = (int64_t)a.H * a.W;
-    const int64_t p = (int64_t)blockIdx.x * THREADS + threadIdx.x;
-    if (p >= (int64_t)a.B * HW) return;
-    const int64_t b = p / HW, pix = p % HW;
+    const int HW = a.H * a.W;
+    const int pix = int(blockIdx.x) * THREADS + int(threadIdx.x);
+    if (pix >= HW) return;
+    const int64_t b = blockIdx.y;
+    const int64_t p = b * HW + pix;
     const int C = a.C;
     const TI *xp = static_cast<const TI *>(a.x) + b * C * HW + pix;
     float kv = 1.f;
     if (a.keep) {
-        const int yy = int(pix / a.W), xx = int(pix % a.W), tw = a.W / a.cell;
+        const int yy = pix / a.W, xx = pix - yy * a.W, tw = a.W / a.cell;
         kv = a.keep[b * (int64_t)(a.H / a.cell) * tw + (yy / a.cell) * tw + xx / a.cell];
     }
-    float v[MAP_MAXC];
+    float v[MC];
+#pragma unroll
+    for (int c = 0; c < MC; ++c) v[c] = ElemIO<TI>::load1(xp + (int64_t)(c < C ? c : C - 1) * HW);
     float s = 0.f;
 #pragma unroll
-    for (int c = 0; c < MAP_MAXC; ++c) {
-        v[c] = c < C ? ElemIO<TI>::load1(xp + c * HW) * kv : 0.f;
+    for (int c = 0; c < MC; ++c) {
+        v[c] = c < C ? v[c] * kv : 0.f;
         s += v[c];
     }
     const float mean = s / float(C);
     float q = 0.f;
 #pragma unroll
-    for (int c = 0; c < MAP_MAXC; ++c) {
+    for (int c = 0; c < MC; ++c) {
         const float d = c < C ? v[c] - mean : 0.f;
         q += d * d;
     }
     const float rstd = rsqrtf(q / float(C) + a.eps);
 #pragma unroll
-    for (int c = 0; c < MAP_MAXC; ++c) {
-        float o = (v[c] - mean) * rstd * (a.w ? a.w[c < C ? c : 0] : 1.f) + (a.b ? a.b[c < C ? c : 0] : 0.f);
-        v[c] = a.gelu ? gelu_erf(o) : o;
+    for (int c = 0; c < MC; ++c) {
+        const int cc = c < C ? c : 0;
+        v[c] = (v[c] - mean) * rstd * (a.w ? a.w[cc] : 1.f) + (a.b ? a.b[cc] : 0.f);
+    }
+    if (a.gelu) {
+#pragma unroll
+        for (int c = 0; c < MC; ++c)
+            if (c < C) v[c] = gelu_erf(v[c]);
     }
     TO *y = static_cast<TO *>(a.y);
     if (a.token_major) {
         TO *yp = y + p * C;
         if (C % 8 == 0) {
 #pragma unroll
-            for (int c0 = 0; c0 < MAP_MAXC; c0 += 8) {
+            for (int c0 = 0; c0 < MC; c0 += 8) {
                 if (c0 >= C) break;
                 float o[8];
 #pragma unroll
@@ -152,14 +164,14 @@ __global__ __launch_bounds__(THREADS) void ln_map_kernel(MapArgs a) {
             }
         } else {
 #pragma unroll
-            for (int c = 0; c < MAP_MAXC; ++c)
+            for (int c = 0; c < MC; ++c)
                 if (c < C) store1(yp + c, v[c]);
         }
     } else {
         TO *yp = y + b * C * HW + pix;
 #pragma unroll
-        for (int c = 0; c < MAP_MAXC; ++c)
-            if (c < C) store1(yp + c * HW, v[c]);
+        for (int c = 0; c < MC; ++c)
+            if (c < C) store1(yp + (int64_t)c * HW, v[c]);
     }
 }
 
@@ -193,11 +205,18 @@ RowsFn pick_rows_o(int odt, int L, int nch) {
     return pick_rows_l<TI, f16_t>(L, nch);
 }
 
+template <typename TI, typename TO>
+MapFn pick_map_c(int C) {
+    if (C <= 16) return reinterpret_cast<MapFn>(ln_map_kernel<TI, TO, 16>);
+    if (C <= 32) return reinterpret_cast<MapFn>(ln_map_kernel<TI, TO, 32>);
+    return reinterpret_cast<MapFn>(ln_map_kernel<TI, TO, MAP_MAXC>);
+}
+
 template <typename TI>
-MapFn pick_map_o(int odt) {
-    if (odt == AFF_F32) return reinterpret_cast<MapFn>(ln_map_kernel<TI, float>);
-    if (odt == AFF_BF16) return reinterpret_cast<MapFn>(ln_map_kernel<TI, bf16_t>);
-    return reinterpret_cast<MapFn>(ln_map_kernel<TI, f16_t>);
+MapFn pick_map_o(int odt, int C) {
+    if (odt == AFF_F32) return pick_map_c<TI, float>(C);
+    if (odt == AFF_BF16) return pick_map_c<TI, bf16_t>(C);
+    return pick_map_c<TI, f16_t>(C);
 }
 
 inline bool dtype_ok(int d) { return d == AFF_F32 || d == AFF_BF16 || d == AFF_F16; }
@@ -249,10 +268,12 @@ extern "C" aff_status aff_layer_norm_map_fwd(const void *x, int x_dtype, void *y
     if (token_major && C % 8 == 0)
         AFF_CHECK_ARG((reinterpret_cast<uintptr_t>(y) & 15) == 0, "aff_layer_norm_map_fwd: y must be 16-byte aligned");
     ln::MapArgs a{x, y, weight, bias, keep, B, C, H, W, keep ? cell : 1, token_major ? 1 : 0, gelu ? 1 : 0, eps};
-    ln::MapFn fn = x_dtype == AFF_F32    ? ln::pick_map_o<float>(y_dtype)
-                   : x_dtype == AFF_BF16 ? ln::pick_map_o<bf16_t>(y_dtype)
-                                         : ln::pick_map_o<f16_t>(y_dtype);
-    hipLaunchKernelGGL(fn, dim3((unsigned)((pix + ln::THREADS - 1) / ln::THREADS)), dim3(ln::THREADS), 0,
-                       static_cast<hipStream_t>(stream), a);
+    ln::MapFn fn = x_dtype == AFF_F32    ? ln::pick_map_o<float>(y_dtype, C)
+                   : x_dtype == AFF_BF16 ? ln::pick_map_o<bf16_t>(y_dtype, C)
+                                         : ln::pick_map_o<f16_t>(y_dtype, C);
+    AFF_CHECK_ARG((int64_t)H * W < ((int64_t)1 << 31) - ln::THREADS && B <= 65535,
+                  "aff_layer_norm_map_fwd: H*W=%lld or B=%d too large", (long long)H * W, B);
+    hipLaunchKernelGGL(fn, dim3((unsigned)(((int64_t)H * W + ln::THREADS - 1) / ln::THREADS), (unsigned)B),
+                       dim3(ln::THREADS), 0, static_cast<hipStream_t>(stream), a);
     return check_launch("aff_layer_norm_map_fwd");
 }

@@ -293,3 +293,37 @@ def test_cluster_attention_module(oracle_mod, dev, with_mask):
     err = float((out - ref).abs().max())
     assert err <= 1e-5 * max(scale, 1.0), f"rel err {err / scale:.3e}"
 
+
+
+def test_cluster_attention_module_bf16(oracle_mod, dev):
+    """ClusterAttention under bf16 autocast (the encoder's mode; with <= 4 heads and no
+    gradient the output projection runs fused in the attention kernel): against the fp64
+    oracle attention on the module's own bf16 q / k / v and the same autocast projection."""
+    from affmae_amd.layers import ClusterAttention
+    B, N, C, H, M = 2, 512, 64, 2, 48
+    Ch = C // H
+    pos = torch.floor(workloads.cfg1_coords(B, N, seed=3) * 32)
+    pos_d = pos.to(dev)
+    idx = knn(pos_d, pos_d, M)
+    idx_np = idx.cpu().numpy()
+    pe = oracle_mod.pe_index(pos.numpy(), idx_np)
+    torch.manual_seed(7)
+    m = ClusterAttention(C, H).to(dev).eval()
+    with torch.no_grad():
+        m.blank_k.normal_(0, 0.3)
+        m.blank_v.normal_(0, 0.3)
+    feat = torch.randn((B, N, C), generator=torch.Generator().manual_seed(9)).to(dev)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        out = m(feat, idx, None, torch.from_numpy(pe).to(dev), False)
+        q = m.q(feat).view(B, N, H, Ch).permute(0, 2, 1, 3)
+        kv = m.kv(feat).view(B, N, H, 2 * Ch).permute(0, 2, 1, 3)
+        assert q.dtype == torch.bfloat16
+        table = m.pos_embed(pre_table_fp32.to(dev)).float()
+        dense = oracle_mod.table_bias(pe, _np(table)).astype(np.float64)
+        ro, _ = oracle_mod.nbhd_attn(_np(q), _np(kv[..., :Ch]), _np(kv[..., Ch:]), idx_np, m.scale, bias=dense,
+                                     blank_k=_np(m.blank_k.view(H, Ch).bfloat16()),
+                                     blank_v=_np(m.blank_v.view(H, Ch).bfloat16()))
+        ref = m.proj(torch.from_numpy(ro.astype(np.float32)).to(dev).permute(0, 2, 1, 3).reshape(B, N, C))
+    assert out.dtype == torch.bfloat16
+    err = float((out.float() - ref.float()).abs().max())
+    assert err <= LOWP_ABS, f"abs err {err:.3e}"

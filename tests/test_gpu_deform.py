@@ -105,6 +105,22 @@ def test_cfg4_multilevel_idw(oracle_mod, dev, B):
     _close(out, ro, torch.bfloat16)
 
 
+def test_cfg4_full_batch_oracle_sample(oracle_mod, dev):
+    """Full config (B=32) against the oracle on three of its images (first, one inside,
+    last) and every 7th query of them: images and queries are computed independently, so
+    the oracle runs on those alone."""
+    w = workloads.cfg4(B=32)
+    out, ki, _ = ms_deformable_attention(w["query_pos"].to(dev), w["kv_pos"].to(dev), w["level_start"],
+                                         w["offsets"].to(dev), w["attn"].to(dev), w["values"].to(dev),
+                                         power=3.0, k=3, weighting="idw", return_knn=True)
+    pick, qs = [0, 13, 31], slice(0, None, 7)
+    sub = lambda t: t[pick][:, qs]
+    ro, ri = oracle_mod.deform(sub(w["query_pos"]).numpy(), w["kv_pos"][pick].numpy(), w["level_start"],
+                               _np(sub(w["offsets"])), _np(sub(w["attn"])), _np(w["values"][pick]), 3.0, 3, "idw")
+    np.testing.assert_array_equal(ki[pick][:, qs].cpu().numpy(), ri)
+    _close(out[pick][:, qs], ro, torch.bfloat16)
+
+
 def test_cfg4_full_batch_consistency(dev):
     """Full config (B=32): images are independent, so images 0-1 of the full
     batch must equal the B=2 run bit for bit; every output finite."""
@@ -200,19 +216,23 @@ def test_level_point_neighbour_shapes(oracle_mod, dev, L, P, K, dtype):
     _close(out, ro, dtype)
 
 
-def test_given_index_kernels(oracle_mod, dev):
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_given_index_kernels(oracle_mod, dev, dtype):
     g = torch.Generator().manual_seed(4)
     B, N, Nkv, K, C = 2, 300, 400, 4, 24
     sl = torch.rand((B, N, 2), generator=g)
     kv = torch.rand((B, Nkv, 2), generator=g)
     idx = knn(sl.to(dev), kv.to(dev), K)
-    aw = torch.rand((B, N), generator=g)
-    val = torch.randn((B, Nkv, C), generator=g)
+    aw = torch.rand((B, N), generator=g).to(dtype)
+    val = torch.randn((B, Nkv, C), generator=g).to(dtype)
     p = torch.tensor(2.5, device=dev)
     out = fused_deformable_attention(sl.to(dev), kv.to(dev), idx, p, aw.to(dev), val.to(dev))
-    rw, ro = oracle_mod.deform_sample(sl.numpy(), kv.numpy(), idx.cpu().numpy(), 2.5, 0, attn=aw.numpy(),
-                                      values=val.numpy())
-    _close(out, ro, torch.float32)
+    assert out.dtype == dtype
+    rw, ro = oracle_mod.deform_sample(sl.numpy(), kv.numpy(), idx.cpu().numpy(), 2.5, 0, attn=_np(aw),
+                                      values=_np(val))
+    _close(out, ro, dtype)
+    if dtype != torch.float32:
+        return
     w = mssample(sl.to(dev), kv.to(dev), idx, p)
     assert w.shape == (B, N, K, 1)
     rw1, _ = oracle_mod.deform_sample(sl.numpy(), kv.numpy(), idx.cpu().numpy(), 2.5, 1)
@@ -286,3 +306,33 @@ def test_deformable_module_against_oracle(oracle_mod, dev, self_attn):
         ref = m.output_proj(torch.from_numpy(ro.astype(np.float32)).to(dev).reshape(b, n_q, d))
     scale = float(ref.abs().max())
     assert float((out - ref).abs().max()) <= 1e-5 * max(scale, 1.0)
+
+
+@pytest.mark.parametrize("self_attn", [False, True])
+def test_deformable_module_bf16_autocast(oracle_mod, dev, self_attn):
+    """The deformable modules under bf16 autocast: against the fp64 oracle on the module's
+    own autocast offsets, attention weights and value projection, followed by the same
+    autocast output projection."""
+    torch.manual_seed(6)
+    d, h, p = 64, 4, 4
+    m = (DeformableSelfAttention if self_attn else DeformableCrossAttention)(d, h, p).to(dev).eval()
+    with torch.no_grad():
+        m.sampling_offsets.weight.normal_(0, 0.02)
+        m.attention_weights.weight.normal_(0, 0.2)
+        m.shepard_power.fill_(1.3)
+    g = torch.Generator().manual_seed(12)
+    q = torch.randn((2, 300, d), generator=g).to(dev)
+    qp = torch.rand((2, 300, 2), generator=g).to(dev)
+    kv = q if self_attn else torch.randn((2, 450, d), generator=g).to(dev)
+    kp = qp if self_attn else torch.rand((2, 450, 2), generator=g).to(dev)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        out = m(q, qp) if self_attn else m(q, qp, kv, kp)
+        b, n_q, n_kv = 2, 300, kv.shape[1]
+        off = m.sampling_offsets(q).view(b, n_q, h, 1, p, 2)
+        att = torch.softmax(m.attention_weights(q).float().view(b, n_q, h, p), -1).view(b, n_q, h, 1, p)
+        val = m.value_proj(kv).view(b, n_kv, h, d // h)
+        assert val.dtype == torch.bfloat16
+        ro, _ = oracle_mod.deform(_np(qp), _np(kp), [0, n_kv], _np(off), _np(att), _np(val), 1.3, 4, "shepard")
+        ref = m.output_proj(torch.from_numpy(ro.astype(np.float32)).to(dev).reshape(b, n_q, d))
+    err = float((out.float() - ref.float()).abs().max())
+    assert err <= 2e-2, f"abs err {err:.3e}"
