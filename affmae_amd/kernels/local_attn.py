@@ -234,7 +234,8 @@ def nbhd_attn_proj_fwd(q, k, v, member_idx, scale, proj_w, proj_b=None, *, pe_id
         out = torch.empty((B, N, C), dtype=q.dtype, device=dev)
     assert tuple(out.shape) == (B, N, C) and out.dtype == q.dtype and out.stride(-1) == 1 and out.stride(1) == C
     w = proj_w.detach().to(q.dtype).contiguous()
-    bias = proj_b.detach().to(torch.float32).contiguous() if proj_b is not None else None
+    # the bias rounded to q's dtype first, as the Linear it replaces adds it with 16-bit operands
+    bias = proj_b.detach().to(q.dtype).to(torch.float32).contiguous() if proj_b is not None else None
     keep += [out, w] + ([bias] if bias is not None else [])
     a.out, a.o_sb, a.o_sh, a.o_sn = out.data_ptr(), out.stride(0), D, C
     st = lib.aff_nbhd_attn_proj_fwd(ctypes.byref(a), w.data_ptr(), bias.data_ptr() if bias is not None else None,

@@ -36,6 +36,9 @@ from ..utils.pos_embed import pre_table_fp16, pre_table_fp32
 class ClusterAttention(nn.Module):
     """Local attention over each token's neighbourhood plus a per-head blank token."""
 
+    # pos_embed builds the bias table in fp32 even under autocast (pe_table)
+    fp32_submodules = ("pos_embed",)
+
     def __init__(self, dim, num_heads, proj_drop=0.):
         super().__init__()
         self.dim = dim

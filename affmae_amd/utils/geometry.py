@@ -102,8 +102,10 @@ def _anchor_grid(n, m, h, w, sf_type):
 def _neighbour_centres(ordered_grid, plw, plh, dev):
     """Patch centres in curve order and those of the previous / next patch on the
     curve, extrapolated at both ends (geometry.py:238-248)."""
-    plhw = torch.tensor([plw, plh], dtype=torch.float32, device=dev)
-    centres = ordered_grid * plhw + plhw / 2 - 0.5
+    # per-column scalars (no host-to-device copy, so the ordering can be graph-captured);
+    # the same fp32 products and sums as with a [plw, plh] tensor
+    centres = torch.stack([ordered_grid[:, 0] * plw + plw / 2 - 0.5, ordered_grid[:, 1] * plh + plh / 2 - 0.5], -1)
+    plhw = (plw, plh)
     npch = centres.shape[0]
     prev_c = torch.zeros_like(centres)
     prev_c[1:] = centres[:npch - 1]
@@ -147,7 +149,7 @@ def _ranking_torch(pos, m, h, w, use_anchor):
         ys, xs = torch.meshgrid(torch.arange(nph, device=dev), torch.arange(npw, device=dev), indexing="ij")
         grid = torch.stack([xs, ys], dim=2).reshape(-1, 2)[order]          # cells in curve order
         plhw, prev_c, next_c = _neighbour_centres(grid, plw, plh, dev)
-        cell = (pos / plhw).floor()
+        cell = (pos / torch.tensor(plhw, dtype=torch.float32, device=dev)).floor()
         cell = (cell[..., 0] + cell[..., 1] * npw).long()                  # row-major patch id
         prank = rank.unsqueeze(0).expand(b, -1).gather(1, cell)             # b x n
         d_prev = (pos - prev_c[prank]).pow(2).sum(-1)

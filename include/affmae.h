@@ -593,7 +593,8 @@ aff_status aff_layer_norm_map_fwd(const void *x, int x_dtype, void *y, int y_dty
  *   maximum over all b, n.  ws: aff_sfc_anchor_workspace_bytes(B, N).
  * aff_sfc_argsort: ranking[b, i] (int64) = the index of the token of rank i in
  *   row b of keys [B, N] (fp32, contiguous), ascending, ties to the lower
- *   index.  ws: aff_sfc_argsort_workspace_bytes(B, N).
+ *   index.  ws: aff_sfc_argsort_workspace_bytes(B, N).  Not for HIP graph
+ *   capture: its radix sort clears state with hipMemsetAsync.
  * ------------------------------------------------------------------------ */
 #define AFF_SFC_MAX_LEVELS 16
 enum { AFF_SFC_SCANLINE = 0, AFF_SFC_PEANO = 1, AFF_SFC_HILBERT = 2 };

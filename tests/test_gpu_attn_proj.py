@@ -2,8 +2,9 @@
 
 Reference: the fp64 oracle attention (oracle.nbhd_attn, pinned in
 tests/test_oracle.py) times the projection weight rounded to the kernel's
-dtype, plus the bias (reference attention.py:204-205 after the local
-attention).  Tolerance: 2e-2 of max|y| (bf16 / fp16: the attention output is
+dtype, plus the bias rounded to that dtype too, as the Linear the kernel
+replaces computes under autocast (reference attention.py:204-205 after the
+local attention).  Tolerance: 2e-2 of max|y| (bf16 / fp16: the attention output is
 rounded to 16 bits before the projection, as the two-step composition does).
 The fused result is also compared with the two-step GPU composition
 (nbhd_attn_fwd, then an fp32 GEMM of its 16-bit output) at 1e-2 of max|y|.
@@ -43,7 +44,7 @@ def _oracle_y(oracle_mod, q, k, v, idx, scale, dense, mask, bk, bv, w, b, dtype)
                                   blank_v=None if bv is None else bv.double().cpu().numpy())
     B, H, N, D = q.shape
     o = torch.from_numpy(out).permute(0, 2, 1, 3).reshape(B, N, H * D)
-    return o @ w.to(dtype).double().T + b.double()
+    return o @ w.to(dtype).double().T + b.to(dtype).double()
 
 
 @pytest.mark.parametrize("H", [1, 2, 4])
@@ -67,7 +68,7 @@ def test_fused_projection(oracle_mod, dev, H, dtype, blank, masked):
         y = nbhd_attn_proj_fwd(q.to(dev), k.to(dev), v.to(dev), idx, scale, w.to(dev), b.to(dev), **args)
     assert y is not None and list(paths) == ["wave+proj"]
     o2, _ = nbhd_attn_fwd(q.to(dev), k.to(dev), v.to(dev), idx, scale, return_lse=False, **args)
-    y2 = o2.permute(0, 2, 1, 3).reshape(B, N, H * 32).float() @ w.to(dtype).float().to(dev).T + b.to(dev)
+    y2 = o2.permute(0, 2, 1, 3).reshape(B, N, H * 32).float() @ w.to(dtype).float().to(dev).T + b.to(dtype).float().to(dev)
     torch.cuda.synchronize()
     dense = oracle_mod.table_bias(pe.cpu().numpy(), table.double().numpy())
     ref = _oracle_y(oracle_mod, q, k, v, idx, scale, dense, None if mask is None else mask.numpy(), bk, bv, w, b,

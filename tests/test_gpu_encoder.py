@@ -263,7 +263,7 @@ def _bf16_attention_checks(oracle_mod, rec, images, expect_paths, paths):
             assert err <= BF16_ABS, f"stage {r['stage']}: attention abs err {err:.3e}"
         else:                             # projection fused in the kernel: y = O W^T + b
             w = a.proj.weight.detach().to(torch.bfloat16).double().cpu()
-            yref = ref @ w.T + _cpu64(a.proj.bias)
+            yref = ref @ w.T + _cpu64(a.proj.bias.detach().to(torch.bfloat16))
             err = float((_cpu64(r["y"][images]) - yref).abs().max())
             assert err <= BF16_ABS * max(1.0, float(yref.abs().max())), f"stage {r['stage']}: fused proj err {err:.3e}"
 
@@ -279,6 +279,26 @@ def test_encoder_bf16_attention_parity(oracle_mod, dev):
     _bf16_attention_checks(oracle_mod, rec, slice(None), FUSED_PATHS, list(paths))
     for i in range(2, 6):
         assert torch.isfinite(out[f"res{i}"]).all()
+
+
+def test_encoder_bf16_stored_weights_match_autocast(dev):
+    """cast_matmul_weights: the encoder with its Linear / convolution weights stored in bf16
+    computes the autocast forward of the fp32-weight encoder (the same products on the same
+    bf16 values; the attention bias table stays fp32)."""
+    from affmae_amd.utils.precision import cast_matmul_weights
+    w = workloads.cfg5(B=2, img=256, seed=13)
+    args = (w["images"].to(dev), w["ids_keep"].to(dev), w["ids_masked"].to(dev), 4)
+    ref_enc, enc16 = _small_encoder(dev), cast_matmul_weights(_small_encoder(dev))
+    assert enc16.layers[0].blocks[0].attn.pos_embed.weight.dtype == torch.float32
+    assert enc16.layers[0].blocks[0].attn.q.weight.dtype == torch.bfloat16
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        ref = workloads.mae_encode(ref_enc, *args)
+        out = workloads.mae_encode(enc16, *args)
+    for i in range(2, 6):
+        a, b = out[f"res{i}"].float(), ref[f"res{i}"].float()
+        assert torch.equal(out[f"res{i}_pos"], ref[f"res{i}_pos"])
+        err = float((a - b).abs().max())
+        assert err <= 1e-3 * max(1.0, float(b.abs().max())), f"res{i}: {err:.3e}"
 
 
 def test_encoder_cfg5_full(oracle_mod, dev):
