@@ -258,16 +258,17 @@ constexpr int MAXM = 64;          // neighbours per query
 constexpr int LPQ = 8;            // set-up lanes per query
 constexpr int RJ = MAXM / LPQ;    // set-up entries per lane: j = jl + 8 r
 constexpr int NW = THREADS / 64;  // waves; wave w takes heads w, w + NW, ...
-constexpr int PWP = UMAX + 4;     // pw row pitch (16-bit codes): 456-byte rows
+constexpr int PWP = UMAX + 4;     // pw row pitch (8-bit codes): 228-byte rows
 constexpr int MAXH = 64;          // heads of this kernel
-constexpr int MAXHM = 192;        // H * M of the per-neighbour bias store
-constexpr int BMW = 2 * MAXH + TQ * MAXHM;  // bias store: fp32 words
+constexpr int MAXHM = 196;        // (M + 1) * HG of the per-neighbour bias store
+constexpr int BMW = TQ * MAXHM;   // bias store: fp32 words
 constexpr int VRP = HD;           // V chunk row pitch (16-bit): 64-byte rows
 constexpr float LOG2E = 1.4426950408889634f;
 static_assert(WWORDS == THREADS, "one bitmap word per thread");
 static_assert(TQ * LPQ == THREADS, "one set-up lane group per query");
-static_assert((TQ * PWP) % 8 == 0, "pw is cleared in 16-byte pieces");
-static_assert(BMW * 4 < 65536, "bias-store byte offsets are 16-bit codes");
+static_assert((TQ * PWP) % 16 == 0 && PWP % 4 == 0, "pw is cleared in 16-byte pieces, read in 4-byte ones");
+static_assert(MAXM + 1 < 256, "a code is an entry number + 1 in 8 bits");
+static_assert(TQ * (NW * HD + 8) * 2 <= BMW * 4, "the projection's output block fits in the bias store");
 }  // namespace wt
 
 // max / sum of v over lanes l and l ^ 32 (v_permlane32_swap exchanges the two halves)
@@ -293,8 +294,9 @@ __device__ __forceinline__ void tile_rows(const aff_nbhd_attn_args &a, int b, in
 }
 
 // Head phase of one wave over a 32-query tile whose union (U rows, ulist), codes (pw)
-// and bias store (bm) are in LDS: heads h0, h0 + hstep, ... below hend.  The bias of
-// head h for a (query, neighbour) code sits at byte 4 * (h - hbase) + code of bm.
+// and bias store (bm) are in LDS: heads h0, h0 + hstep, ... below hend.  Query q's
+// block of bm holds (M + 1) entries of HG heads, entry 0 the -inf one; a (query, slot)
+// code c (8 bits: 0 or neighbour entry + 1) puts head h's bias at entry c of the block.
 // nm: masked (live) neighbours of this lane's query; vbuf: the wave's V chunk buffer.
 //
 // Per 32-slot chunk:
@@ -311,8 +313,8 @@ __device__ __forceinline__ void tile_rows(const aff_nbhd_attn_args &a, int b, in
 // yo[4 j + i]) stay in registers for the projection epilogue instead of going to out.
 template <typename T, bool BLANK, bool STAGE = false>
 __device__ __forceinline__ void wave_head_one(const aff_nbhd_attn_args &a, int b, int n0, int U, const int *ulist,
-                                              const uint16_t *pw, const float *bm, float nm, uint16_t *vbuf, int h,
-                                              int hbase, float *yo = nullptr) {
+                                              const uint8_t *pw, const float *bm, float nm, uint16_t *vbuf, int h,
+                                              int hbase, int HG, float *yo = nullptr) {
     using namespace wt;
     using MM = Mfma32<T>;
     const int lane = threadIdx.x & 63;
@@ -329,8 +331,9 @@ __device__ __forceinline__ void wave_head_one(const aff_nbhd_attn_args &a, int b
     const float scale2 = a.scale * LOG2E;
     // transposing-read role: 16-lane group g reads channels 16 (g & 1) + (lane & 15)
     const int kk = (lane & 15) >> 2, aa = lane & 3, cg = 16 * ((lane >> 4) & 1);
-    const uint16_t *pwrow = pw + ql * PWP + 4 * hh;
-    const uint32_t vst0 = (lane >> 2) * VRP + (lane & 3) * 8, vst1 = vst0 + 16 * VRP;
+    const uint8_t *pwrow = pw + ql * PWP + 4 * hh;
+    // V rows go through a 16-row buffer: rows 0..15 of the chunk, then rows 16..31
+    const uint32_t vst0 = (lane >> 2) * VRP + (lane & 3) * 8;
     const uint16_t *vtr = vbuf + (4 * hh + kk) * VRP + cg + 4 * aa;
     // K row of this lane in chunk c: union slot 32 c + ql; V pieces p = lane + 64 i: row p >> 2, bytes 16 (p & 3)
     auto koff = [&](int c) {
@@ -376,52 +379,50 @@ __device__ __forceinline__ void wave_head_one(const aff_nbhd_attn_args &a, int b
             sb = pair_sum(part) * scale2;
             m = fmaxf(m, sb);
         }
-        const char *bmh = reinterpret_cast<const char *>(bm) + 4 * (h - hbase);
+        const char *bmh = reinterpret_cast<const char *>(bm) + 4 * (ql * (a.M + 1) * HG + (h - hbase));
+        const uint32_t cstep = 4 * HG;  // bytes per code step
         float lp = 0.f;
         f32x16 O;
 #pragma unroll
         for (int r = 0; r < 16; ++r) O[r] = 0.f;
 
         // LDS data of the lane's 16 slots (8 j + 4 hh + i of a chunk): the codes are read
-        // two chunks ahead and the biases one chunk ahead of their use
-        auto read_codes = [&](int c, uint32_t (&cw)[8]) {
+        // one chunk ahead, the biases at the start of their chunk (read during the S
+        // MFMAs; no bias registers are held across chunks)
+        auto read_codes = [&](int c, uint32_t (&cw)[4]) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint2 v = *reinterpret_cast<const uint2 *>(pwrow + 32 * c + 8 * j);
-                cw[2 * j] = v.x;
-                cw[2 * j + 1] = v.y;
-            }
+            for (int j = 0; j < 4; ++j) cw[j] = *reinterpret_cast<const uint32_t *>(pwrow + 32 * c + 8 * j);
         };
-        auto read_bias = [&](const uint32_t (&cw)[8], float (&bias)[16]) {
+        auto read_bias = [&](const uint32_t (&cw)[4], float (&bias)[16]) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const uint32_t code = (r & 1) ? (cw[r >> 1] >> 16) : (cw[r >> 1] & 0xffffu);
-                bias[r] = *reinterpret_cast<const float *>(bmh + code);
+                const uint32_t code = (cw[r >> 2] >> (8 * (r & 3))) & 0xffu;
+                bias[r] = *reinterpret_cast<const float *>(bmh + __umul24(code, cstep));
             }
         };
-        uint32_t cwA[8], cwB[8];
-        float bA[16], bB[16];
-        if (nch > 0) {
-            read_codes(0, cwA);
-            read_bias(cwA, bA);
-            read_codes(min(1, nch - 1), cwB);
-        }
+        uint32_t cwA[4], cwB[4];
+        if (nch > 0) read_codes(0, cwA);
 
-        // chunk c: K/V registers k0..v1, biases bc; codes of chunk c + 1 in cn (their
-        // biases go to bn) and the codes of chunk c + 2 replace cc
-        auto chunk = [&](int c, const uint4 &k0, const uint4 &k1, const uint4 &v0, const uint4 &v1, const float (&bc)[16],
-                         uint32_t (&cc)[8], const uint32_t (&cn)[8], float (&bn)[16]) {
-            // this chunk's V rows into the wave's buffer and their transposed reads (the
-            // previous chunk's reads are done: LDS operations of one wave complete in order)
+        // chunk c: K/V registers k0..v1, codes cc; the codes of chunk c + 1 go to cn
+        auto chunk = [&](int c, const uint4 &k0, const uint4 &k1, const uint4 &v0, const uint4 &v1,
+                         const uint32_t (&cc)[4], uint32_t (&cn)[4]) {
+            // this chunk's V rows through the wave's 16-row buffer and their transposed
+            // reads, rows 0..15 then 16..31 (a wave's LDS operations complete in order, so
+            // each store follows the reads issued before it)
+            uint2 vt[4];
             asm volatile("" ::: "memory");
             *reinterpret_cast<uint4 *>(vbuf + vst0) = v0;
-            *reinterpret_cast<uint4 *>(vbuf + vst1) = v1;
             asm volatile("" ::: "memory");
-            uint2 vt[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) vt[i] = lds_read_tr16(vtr + (8 * i) * VRP);
-            read_bias(cn, bn);
-            read_codes(min(c + 2, nch - 1), cc);
+            vt[0] = lds_read_tr16(vtr);
+            vt[1] = lds_read_tr16(vtr + 8 * VRP);
+            asm volatile("" ::: "memory");
+            *reinterpret_cast<uint4 *>(vbuf + vst0) = v1;
+            asm volatile("" ::: "memory");
+            vt[2] = lds_read_tr16(vtr);
+            vt[3] = lds_read_tr16(vtr + 8 * VRP);
+            float bc[16];
+            read_bias(cc, bc);
+            read_codes(min(c + 1, nch - 1), cn);
             f32x16 S;
 #pragma unroll
             for (int r = 0; r < 16; ++r) S[r] = 0.f;
@@ -465,10 +466,10 @@ __device__ __forceinline__ void wave_head_one(const aff_nbhd_attn_args &a, int b
         // chunk's MFMAs on every path, serialising load latency with compute.
         for (int c = 0; c < nch; c += 2) {
             fetch(min(c + 1, nch - 1), kB0, kB1, vB0, vB1);
-            chunk(c, kA0, kA1, vA0, vA1, bA, cwA, cwB, bB);
+            chunk(c, kA0, kA1, vA0, vA1, cwA, cwB);
             if (c + 1 >= nch) break;
             fetch(min(c + 2, nch - 1), kA0, kA1, vA0, vA1);
-            chunk(c + 1, kB0, kB1, vB0, vB1, bB, cwB, cwA, bA);
+            chunk(c + 1, kB0, kB1, vB0, vB1, cwB, cwA);
         }
 
         // ---- normalise, blank value, store: channels 8 j + 4 hh + i of query ql
@@ -518,9 +519,9 @@ __device__ __forceinline__ void wave_head_one(const aff_nbhd_attn_args &a, int b
 // Heads h0, h0 + hstep, ... below hend, one after another (wave_head_one).
 template <typename T, bool BLANK>
 __device__ __forceinline__ void wave_heads(const aff_nbhd_attn_args &a, int b, int n0, int U, const int *ulist,
-                                           const uint16_t *pw, const float *bm, float nm, uint16_t *vbuf, int h0,
-                                           int hstep, int hend, int hbase) {
-    for (int h = h0; h < hend; h += hstep) wave_head_one<T, BLANK>(a, b, n0, U, ulist, pw, bm, nm, vbuf, h, hbase);
+                                           const uint8_t *pw, const float *bm, float nm, uint16_t *vbuf, int h0,
+                                           int hstep, int hend, int hbase, int HG) {
+    for (int h = h0; h < hend; h += hstep) wave_head_one<T, BLANK>(a, b, n0, U, ulist, pw, bm, nm, vbuf, h, hbase, HG);
 }
 
 // The output projection fused into the wave kernel's epilogue (ClusterAttention's
@@ -567,25 +568,25 @@ __device__ __forceinline__ void proj_epilogue(const aff_nbhd_attn_args &a, const
 }
 
 template <typename T, int BIAS, bool IDX64, bool BLANK, bool PROJ = false>
-__global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nbhd_attn_args a, int HG,
+__global__ __launch_bounds__(THREADS, 4) void nbhd_attn_wave_kernel(const aff_nbhd_attn_args a, int HG,
                                                                     const ProjArgs pj) {
     using namespace wt;
     using MM = Mfma32<T>;
-    // pw[q][slot]: byte offset in bm of the (query, neighbour) pair's biases; 0 (the
-    // -inf entry) where the union slot is not one of the query's neighbours
-    __shared__ __align__(16) uint16_t pw[TQ * PWP];
-    // bm: biases of this workgroup's head group, times log2(e): [HG] -inf, [HG] zero,
-    // then [TQ][M][HG]
+    // pw[q][slot]: 1 + the neighbour entry of query q whose row is union slot `slot`; 0
+    // where the slot is not one of the query's neighbours
+    __shared__ __align__(16) uint8_t pw[TQ * PWP];
+    // bm: biases of this workgroup's head group, times log2(e): [TQ][M + 1][HG], entry 0
+    // of each query -inf, entry 1 + j neighbour j.  The LDS of a workgroup stays under
+    // 40 KB, so that four fit on a CU.
     __shared__ __align__(16) float bm[BMW];
     __shared__ int ulist[UMAX];
     struct SetupLds {
-        uint8_t flg[WWORDS * 32];  // one byte per index of the window: a neighbour row
-        uint32_t bits[WWORDS];     // the same flags packed 32 to a word
-        uint32_t pref[WWORDS];     // union slots before each word
+        uint32_t bits[WWORDS];  // one bit per index of the window: a neighbour row
+        uint32_t pref[WWORDS];  // union slots before each word
     };
     __shared__ __align__(16) union {
         SetupLds s;
-        uint16_t vb[NW][32 * VRP];  // per-wave V chunk (head phase)
+        uint16_t vb[NW][16 * VRP];  // per-wave 16-row V buffer (head phase)
     } sh;
     __shared__ float nmq_s[TQ];
     __shared__ int red[4];  // 0 flagged, 1 repeated index, 2 U
@@ -607,12 +608,9 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
     const int nr = (M + LPQ - 1) / LPQ;  // entries per set-up lane that exist (uniform)
 
     if (t < 4) red[t] = 0;
-    for (int i = t; i < WWORDS * 2; i += THREADS) reinterpret_cast<uint4 *>(sh.s.flg)[i] = make_uint4(0, 0, 0, 0);
-    for (int i = t; i < TQ * PWP / 8; i += THREADS) reinterpret_cast<uint4 *>(pw)[i] = make_uint4(0, 0, 0, 0);
-    if (t < HG) {
-        bm[t] = -INFINITY;
-        bm[HG + t] = 0.f;
-    }
+    sh.s.bits[t] = 0u;  // WWORDS == THREADS
+    for (int i = t; i < TQ * PWP / 16; i += THREADS) reinterpret_cast<uint4 *>(pw)[i] = make_uint4(0, 0, 0, 0);
+    for (int i = t; i < TQ * HG; i += THREADS) bm[(i / HG) * (M + 1) * HG + i % HG] = -INFINITY;
 
     // ---- this lane's (query, neighbour) entries j = jl + 8 r.  Loads are unconditional
     // buffer loads at 32-bit offsets inside this image's planes (clamped to entry M - 1
@@ -659,7 +657,7 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
     // are loaded here and stay in flight through the union steps; the rows are read
     // and bm written after the slots (write_table_biases).  Modes 1 and 3 store at
     // once; mode 0 stores zeros.
-    const int rowq_b = 2 * HG + q * M * HG;  // bm word of (q, j = 0, group head 0)
+    const int rowq_b = (q * (M + 1) + 1) * HG;  // bm word of (q, j = 0, group head 0)
     const bool fast4 = (BIAS == 2 || BIAS == 4) && HG == 4 && H % 4 == 0 && a.table_dtype == AFF_F32;
     float2 gq[RJ];   // BIAS 4: neighbour coordinates
     int64_t prow[RJ];  // BIAS 2: pe rows
@@ -748,12 +746,12 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
             }
         }
     };
-    // the cleared flags are visible before any wave sets one (the loads above stay
+    // the cleared bits are visible before any wave sets one (the loads above stay
     // in flight across this barrier)
     lds_barrier();
 
-    // ---- union: a flag byte per neighbour row of the index window [wlo, wlo + 8192)
-    // (plain stores: every writer of a byte writes the same 1)
+    // ---- union: a bit per neighbour row of the index window [wlo, wlo + 8192), set with
+    // LDS atomic ORs (no return value)
     const int wlo = max(0, min(n0 + TQ / 2 - WWORDS * 16, N - WWORDS * 32));
     bool outside = false;
 #pragma unroll
@@ -762,7 +760,7 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
         const unsigned o = unsigned(idx[r] - wlo);
         const bool in = o < unsigned(WWORDS * 32);
         outside = outside || (use[r] && !in);
-        if (use[r] && in) sh.s.flg[o] = 1;
+        if (use[r] && in) atomicOr(&sh.s.bits[o >> 5], 1u << (o & 31));
     }
     if (outside) red[0] = 1;
     {
@@ -771,18 +769,7 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
     }
     lds_barrier();
 
-    // ---- flags -> bits (thread t packs window word t)
-    {
-        const uint4 f0 = reinterpret_cast<const uint4 *>(sh.s.flg)[2 * t];
-        const uint4 f1 = reinterpret_cast<const uint4 *>(sh.s.flg)[2 * t + 1];
-        const uint32_t d[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
-        uint32_t wbits = 0;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) wbits |= (((d[k] * 0x01020408u) >> 24) & 0xFu) << (4 * k);  // 4 flag bytes -> 4 bits
-        sh.s.bits[t] = wbits;
-    }
     load_table_rows();
-    lds_barrier();
 
     const bool flagged = (a.mask && a.mask_sh != 0) || red[0] != 0;
     if (!flagged && w == 0) {
@@ -825,7 +812,7 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
             slot[r] = s_;
             if (use[r]) {
                 ulist[s_] = idx[r];
-                pw[rowq + s_] = uint16_t(uint32_t(rowq_b + (jl + LPQ * r) * HG) * 4);
+                pw[rowq + s_] = uint8_t(jl + LPQ * r + 1);
             }
         }
         write_table_biases();
@@ -837,7 +824,7 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
 #pragma unroll
         for (int r = 0; r < RJ; ++r)
             if (r < nr && use[r])
-                dup = dup || pw[rowq + slot[r]] != uint16_t(uint32_t(rowq_b + (jl + LPQ * r) * HG) * 4);
+                dup = dup || pw[rowq + slot[r]] != uint8_t(jl + LPQ * r + 1);
         if (__builtin_amdgcn_ballot_w64(dup) != 0 && lane == 0) red[1] = 1;
         lds_barrier();
         fallback = red[1] != 0;
@@ -849,7 +836,7 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
             return;
         }
         // ---- head phase: wave w, heads hb + w, hb + w + NW, ... of the group
-        wave_heads<T, BLANK>(a, b, n0, U, ulist, pw, bm, nmq_s[lane & 31], sh.vb[w], hb + w, NW, hb + hn, hb);
+        wave_heads<T, BLANK>(a, b, n0, U, ulist, pw, bm, nmq_s[lane & 31], sh.vb[w], hb + w, NW, hb + hn, hb, HG);
     } else {
         // every head of the image in this workgroup, at most one per wave (host-checked);
         // the [32][C] output block is staged in bm's space once every wave is past it
@@ -872,7 +859,7 @@ __global__ __launch_bounds__(THREADS, 3) void nbhd_attn_wave_kernel(const aff_nb
             float yo[16];
             const bool has = w < H;
             if (has)
-                wave_head_one<T, BLANK, true>(a, b, n0, U, ulist, pw, bm, nmq_s[lane & 31], sh.vb[w], w, 0, yo);
+                wave_head_one<T, BLANK, true>(a, b, n0, U, ulist, pw, bm, nmq_s[lane & 31], sh.vb[w], w, 0, HG, yo);
             __syncthreads();
             if (has) {
                 const int hh = lane >> 5, ql = lane & 31;
@@ -923,9 +910,9 @@ inline int64_t tile_count(const aff_nbhd_attn_args &a) {
 // The wave-per-head kernel: 16-bit q/k/v, head_dim 32, M <= 64, every bias mode and
 // head count, 32-bit offsets inside one image's q/k/v, index and mask planes.  One
 // workgroup per (tile, head group) of wave_heads_per_group() heads: the group's
-// per-(query, neighbour) bias store, TQ * M * HG fp32 words, stays within MAXHM
-// per query (its 16-bit byte offsets) and the extra workgroups fill the chip when
-// a stage has few tiles and many heads.
+// per-(query, neighbour) bias store, TQ * (M + 1) * HG fp32 words, stays within
+// MAXHM per query and the extra workgroups fill the chip when a stage has few tiles
+// and many heads.
 inline bool use_wave_path(const aff_nbhd_attn_args &a) {
     if (a.dtype == AFF_F32 || a.D != wt::HD || a.M > wt::MAXM) return false;
     // 32-bit byte offsets inside one (b, h) plane, built with 24-bit multiplies
@@ -940,9 +927,9 @@ inline bool use_wave_path(const aff_nbhd_attn_args &a) {
     return true;
 }
 
-// Heads per workgroup of the wave kernel: at most MAXHM / M (the bias store) and MAXH.
+// Heads per workgroup of the wave kernel: at most MAXHM / (M + 1) (the bias store) and MAXH.
 inline int wave_heads_per_group(const aff_nbhd_attn_args &a) {
-    int hg = a.M > 0 ? wt::MAXHM / a.M : wt::MAXH;
+    int hg = wt::MAXHM / (a.M + 1);
     hg = hg < 1 ? 1 : (hg > wt::MAXH ? wt::MAXH : hg);
     return a.H < hg ? a.H : hg;
 }
@@ -1052,7 +1039,7 @@ extern "C" aff_status aff_nbhd_attn_proj_fwd(const aff_nbhd_attn_args *args, con
         a.H > attn::wt::NW || attn::wave_heads_per_group(a) < a.H)
         return fail(AFF_ERR_UNSUPPORTED,
                     "aff_nbhd_attn_proj_fwd: needs 16-bit q/k/v, head_dim 32, at most %d heads and M <= %d (H=%d M=%d D=%d)",
-                    attn::wt::NW, attn::wt::MAXHM / (a.H > 0 ? a.H : 1), a.H, a.M, a.D);
+                    attn::wt::NW, attn::wt::MAXHM / (a.H > 0 ? a.H : 1) - 1, a.H, a.M, a.D);
     AFF_CHECK_ARG(proj_w && attn::aligned16(proj_w), "aff_nbhd_attn_proj_fwd: proj_w NULL or not 16-byte aligned");
     AFF_CHECK_ARG(a.o_sh == a.D && a.o_sn >= (int64_t)a.H * a.D,
                   "aff_nbhd_attn_proj_fwd: out must be [B, N, H * D] rows (o_sh = D)");
