@@ -608,9 +608,22 @@ __global__ __launch_bounds__(THREADS, 4) void nbhd_attn_wave_kernel(const aff_nb
     const int nr = (M + LPQ - 1) / LPQ;  // entries per set-up lane that exist (uniform)
 
     if (t < 4) red[t] = 0;
-    sh.s.bits[t] = 0u;  // WWORDS == THREADS
+    // Table bias modes write the bias store only after the slots step, so their union flags
+    // (a byte per window index, plain stores) live in its space until then; the other modes
+    // write biases while loading the entries and set the union bits with LDS atomics.
+    constexpr bool FLAGS = BIAS == 2 || BIAS == 4;
+    static_assert(WWORDS * 32 <= BMW * 4, "the union flags fit in the bias store");
+    uint8_t *flg = reinterpret_cast<uint8_t *>(bm);
+    auto init_inf = [&]() {
+        for (int i = t; i < TQ * HG; i += THREADS) bm[(i / HG) * (M + 1) * HG + i % HG] = -INFINITY;
+    };
+    if constexpr (FLAGS) {
+        for (int i = t; i < WWORDS * 2; i += THREADS) reinterpret_cast<uint4 *>(flg)[i] = make_uint4(0, 0, 0, 0);
+    } else {
+        sh.s.bits[t] = 0u;  // WWORDS == THREADS
+        init_inf();
+    }
     for (int i = t; i < TQ * PWP / 16; i += THREADS) reinterpret_cast<uint4 *>(pw)[i] = make_uint4(0, 0, 0, 0);
-    for (int i = t; i < TQ * HG; i += THREADS) bm[(i / HG) * (M + 1) * HG + i % HG] = -INFINITY;
 
     // ---- this lane's (query, neighbour) entries j = jl + 8 r.  Loads are unconditional
     // buffer loads at 32-bit offsets inside this image's planes (clamped to entry M - 1
@@ -750,8 +763,8 @@ __global__ __launch_bounds__(THREADS, 4) void nbhd_attn_wave_kernel(const aff_nb
     // in flight across this barrier)
     lds_barrier();
 
-    // ---- union: a bit per neighbour row of the index window [wlo, wlo + 8192), set with
-    // LDS atomic ORs (no return value)
+    // ---- union: a flag byte (table modes) or bit per neighbour row of the index window
+    // [wlo, wlo + 8192)
     const int wlo = max(0, min(n0 + TQ / 2 - WWORDS * 16, N - WWORDS * 32));
     bool outside = false;
 #pragma unroll
@@ -760,7 +773,10 @@ __global__ __launch_bounds__(THREADS, 4) void nbhd_attn_wave_kernel(const aff_nb
         const unsigned o = unsigned(idx[r] - wlo);
         const bool in = o < unsigned(WWORDS * 32);
         outside = outside || (use[r] && !in);
-        if (use[r] && in) atomicOr(&sh.s.bits[o >> 5], 1u << (o & 31));
+        if (use[r] && in) {
+            if constexpr (FLAGS) flg[o] = 1;  // every writer of a byte writes the same 1
+            else atomicOr(&sh.s.bits[o >> 5], 1u << (o & 31));
+        }
     }
     if (outside) red[0] = 1;
     {
@@ -769,7 +785,22 @@ __global__ __launch_bounds__(THREADS, 4) void nbhd_attn_wave_kernel(const aff_nb
     }
     lds_barrier();
 
-    load_table_rows();
+    if constexpr (FLAGS) {
+        // flags -> bits (thread t packs window word t); the -inf entries then take the
+        // flags' place once every wave is past them
+        const uint4 f0 = reinterpret_cast<const uint4 *>(flg)[2 * t];
+        const uint4 f1 = reinterpret_cast<const uint4 *>(flg)[2 * t + 1];
+        const uint32_t d[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+        uint32_t wbits = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) wbits |= (((d[k] * 0x01020408u) >> 24) & 0xFu) << (4 * k);  // 4 flag bytes -> 4 bits
+        sh.s.bits[t] = wbits;
+        load_table_rows();
+        lds_barrier();
+        init_inf();
+    } else {
+        load_table_rows();
+    }
 
     const bool flagged = (a.mask && a.mask_sh != 0) || red[0] != 0;
     if (!flagged && w == 0) {
