@@ -294,9 +294,10 @@ __device__ __forceinline__ void tile_rows(const aff_nbhd_attn_args &a, int b, in
 }
 
 // Head phase of one wave over a 32-query tile whose union (U rows, ulist), codes (pw)
-// and bias store (bm) are in LDS: heads h0, h0 + hstep, ... below hend.  Query q's
-// block of bm holds (M + 1) entries of HG heads, entry 0 the -inf one; a (query, slot)
-// code c (8 bits: 0 or neighbour entry + 1) puts head h's bias at entry c of the block.
+// and bias store (bm) are in LDS: heads h0, h0 + hstep, ... below hend.  bm holds a plane
+// per head of the group, (M + 1) entries per query, entry 0 the -inf one; a (query, slot)
+// code c (8 bits: 0 or neighbour entry + 1) puts head h's bias at entry c of the query's
+// row in head h's plane.
 // nm: masked (live) neighbours of this lane's query; vbuf: the wave's V chunk buffer.
 //
 // Per 32-slot chunk:
@@ -379,8 +380,8 @@ __device__ __forceinline__ void wave_head_one(const aff_nbhd_attn_args &a, int b
             sb = pair_sum(part) * scale2;
             m = fmaxf(m, sb);
         }
-        const char *bmh = reinterpret_cast<const char *>(bm) + 4 * (ql * (a.M + 1) * HG + (h - hbase));
-        const uint32_t cstep = 4 * HG;  // bytes per code step
+        // head-major planes [HG][TQ][M + 1]: the lanes of one wave (one head) spread over all banks
+        const char *bmh = reinterpret_cast<const char *>(bm) + 4 * (((h - hbase) * TQ + ql) * (a.M + 1));
         float lp = 0.f;
         f32x16 O;
 #pragma unroll
@@ -397,7 +398,7 @@ __device__ __forceinline__ void wave_head_one(const aff_nbhd_attn_args &a, int b
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const uint32_t code = (cw[r >> 2] >> (8 * (r & 3))) & 0xffu;
-                bias[r] = *reinterpret_cast<const float *>(bmh + __umul24(code, cstep));
+                bias[r] = *reinterpret_cast<const float *>(bmh + 4 * code);
             }
         };
         uint32_t cwA[4], cwB[4];
@@ -575,8 +576,8 @@ __global__ __launch_bounds__(THREADS, 4) void nbhd_attn_wave_kernel(const aff_nb
     // pw[q][slot]: 1 + the neighbour entry of query q whose row is union slot `slot`; 0
     // where the slot is not one of the query's neighbours
     __shared__ __align__(16) uint8_t pw[TQ * PWP];
-    // bm: biases of this workgroup's head group, times log2(e): [TQ][M + 1][HG], entry 0
-    // of each query -inf, entry 1 + j neighbour j.  The LDS of a workgroup stays under
+    // bm: biases of this workgroup's head group, times log2(e): [HG][TQ][M + 1], entry 0
+    // of each (head, query) -inf, entry 1 + j neighbour j.  The LDS of a workgroup stays under
     // 40 KB, so that four fit on a CU.
     __shared__ __align__(16) float bm[BMW];
     __shared__ int ulist[UMAX];
@@ -615,7 +616,7 @@ __global__ __launch_bounds__(THREADS, 4) void nbhd_attn_wave_kernel(const aff_nb
     static_assert(WWORDS * 32 <= BMW * 4, "the union flags fit in the bias store");
     uint8_t *flg = reinterpret_cast<uint8_t *>(bm);
     auto init_inf = [&]() {
-        for (int i = t; i < TQ * HG; i += THREADS) bm[(i / HG) * (M + 1) * HG + i % HG] = -INFINITY;
+        for (int i = t; i < TQ * HG; i += THREADS) bm[i * (M + 1)] = -INFINITY;  // (head, query) = (i / TQ, i % TQ)
     };
     if constexpr (FLAGS) {
         for (int i = t; i < WWORDS * 2; i += THREADS) reinterpret_cast<uint4 *>(flg)[i] = make_uint4(0, 0, 0, 0);
@@ -670,7 +671,8 @@ __global__ __launch_bounds__(THREADS, 4) void nbhd_attn_wave_kernel(const aff_nb
     // are loaded here and stay in flight through the union steps; the rows are read
     // and bm written after the slots (write_table_biases).  Modes 1 and 3 store at
     // once; mode 0 stores zeros.
-    const int rowq_b = (q * (M + 1) + 1) * HG;  // bm word of (q, j = 0, group head 0)
+    const int PL = TQ * (M + 1);             // bm words per head plane
+    const int rowq_b = q * (M + 1) + 1;      // bm word of (q, j = 0) in head 0's plane
     const bool fast4 = (BIAS == 2 || BIAS == 4) && HG == 4 && H % 4 == 0 && a.table_dtype == AFF_F32;
     float2 gq[RJ];   // BIAS 4: neighbour coordinates
     int64_t prow[RJ];  // BIAS 2: pe rows
@@ -699,22 +701,22 @@ __global__ __launch_bounds__(THREADS, 4) void nbhd_attn_wave_kernel(const aff_nb
             }
         } else if constexpr (BIAS == 1) {
             if (use[r]) {
-                float *dst = bm + rowq_b + j * HG;
+                float *dst = bm + rowq_b + j;
                 const int64_t e = (int64_t)b * a.bias_sb + (int64_t)nc * a.bias_sn + j;
                 for (int h = 0; h < hn; ++h)
-                    dst[h] = load_any(a.bias, a.bias_dtype, e + (int64_t)(hb + h) * a.bias_sh) * LOG2E;
+                    dst[h * PL] = load_any(a.bias, a.bias_dtype, e + (int64_t)(hb + h) * a.bias_sh) * LOG2E;
             }
         } else if constexpr (BIAS == 3) {
             if (use[r]) {
-                float *dst = bm + rowq_b + j * HG;
+                float *dst = bm + rowq_b + j;
                 const float2 g = *reinterpret_cast<const float2 *>(pos_b + (int64_t)idx[r] * a.pos_sn);
                 for (int h = 0; h < hn; ++h)
-                    dst[h] = cont_bias(a.pos_w + (hb + h) * 5, a.pos_b[hb + h], g.x - pqx, g.y - pqy) * LOG2E;
+                    dst[h * PL] = cont_bias(a.pos_w + (hb + h) * 5, a.pos_b[hb + h], g.x - pqx, g.y - pqy) * LOG2E;
             }
         } else {
             // no bias: zero entries, so that every (query, neighbour) pair still has its own code
             if (use[r])
-                for (int h = 0; h < hn; ++h) bm[rowq_b + j * HG + h] = 0.f;
+                for (int h = 0; h < hn; ++h) bm[h * PL + rowq_b + j] = 0.f;
         }
     }
     auto table_row = [&](int r) -> int64_t {
@@ -746,15 +748,18 @@ __global__ __launch_bounds__(THREADS, 4) void nbhd_attn_wave_kernel(const aff_nb
 #pragma unroll
             for (int r = 0; r < RJ; ++r) {
                 if (r >= nr || !use[r]) continue;
-                float *dst = bm + rowq_b + (jl + LPQ * r) * HG;
+                float *dst = bm + rowq_b + (jl + LPQ * r);
                 if (fast4) {
                     const float sc = tsc[r];
-                    *reinterpret_cast<float4 *>(dst) = make_float4(tv[r].x * sc, tv[r].y * sc, tv[r].z * sc, tv[r].w * sc);
+                    dst[0] = tv[r].x * sc;
+                    dst[PL] = tv[r].y * sc;
+                    dst[2 * PL] = tv[r].z * sc;
+                    dst[3 * PL] = tv[r].w * sc;
                 } else {
                     const int64_t row = table_row(r);
                     const bool in = row >= 0 && row < a.table_rows;
                     for (int h = 0; h < hn; ++h)
-                        dst[h] = in ? load_any(a.table, a.table_dtype, row * H + hb + h) * LOG2E : 0.f;
+                        dst[h * PL] = in ? load_any(a.table, a.table_dtype, row * H + hb + h) * LOG2E : 0.f;
                 }
             }
         }
