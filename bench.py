@@ -9,10 +9,12 @@ bias (Linear(5,4) applied to the reference's offset table, the row chosen
 in-kernel from the two coordinates).  One step = aff_knn + aff_nbhd_attn_fwd
 over the whole batch with every input already resident in HBM.
 
-Prints one JSON line.  ``value`` is tokens/s through the whole step;
-``roofline`` is for the attention kernel (the dominant one), with its
-average launch duration measured by HIP events on the launch stream inside
-the timed region; ``cpu_baseline`` times the reference's own PyTorch path in
+Prints one JSON line.  ``value`` is tokens/s through the whole step, from
+the wall clock around K steps (after W warm-up steps, synchronised on both
+sides); ``roofline`` is for the attention kernel (the dominant one), with its
+average launch duration measured by HIP events on the launch stream in a
+second run of the same K steps (events recorded between the kernels would
+add their host cost to the headline steps); ``cpu_baseline`` times the reference's own PyTorch path in
 torch-CPU fp32 (oracle/torch_path.py) on the same images on this host.  The
 HBM traffic and SQ-counter figures come from the committed rocprofv3
 summaries under profiles/ and are null when the kernel source has changed
@@ -419,9 +421,14 @@ def main() -> int:
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(K):
-        step(i)
+        step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
+    # the per-kernel HIP events go in a second run of the same K steps: recording them
+    # inside the headline loop adds about 10 us of host work to each 0.23 ms step
+    for i in range(K):
+        step(i)
+    torch.cuda.synchronize()
 
     sec = t1 - t0
     ms_step = sec / K * 1e3
