@@ -315,7 +315,7 @@ __device__ __forceinline__ void tile_rows(const aff_nbhd_attn_args &a, int b, in
 template <typename T, bool BLANK, bool STAGE = false>
 __device__ __forceinline__ void wave_head_one(const aff_nbhd_attn_args &a, int b, int n0, int U, const int *ulist,
                                               const uint8_t *pw, const float *bm, float nm, uint16_t *vbuf, int h,
-                                              int hbase, int HG, float *yo = nullptr) {
+                                              int hbase, int HG, float *yo = nullptr, int qlo = 0, int qhi = wt::TQ) {
     using namespace wt;
     using MM = Mfma32<T>;
     const int lane = threadIdx.x & 63;
@@ -325,7 +325,7 @@ __device__ __forceinline__ void wave_head_one(const aff_nbhd_attn_args &a, int b
     };
     const int hh = lane >> 5, ql = lane & 31;
     const int nch = (U + 31) >> 5;
-    const bool qout = n0 + ql < N;
+    const bool qout = n0 + ql < N && ql >= qlo && ql < qhi;  // rows this call stores
     const int qrow = min(n0 + ql, N - 1);
     const uint32_t ksn2 = uint32_t(a.k_sn * 2), vsn2 = uint32_t(a.v_sn * 2);  // < 2^24, host-checked
     const uint32_t qoff = uint32_t(qrow) * uint32_t(a.q_sn * 2) + 32 * hh;
@@ -521,8 +521,9 @@ __device__ __forceinline__ void wave_head_one(const aff_nbhd_attn_args &a, int b
 template <typename T, bool BLANK>
 __device__ __forceinline__ void wave_heads(const aff_nbhd_attn_args &a, int b, int n0, int U, const int *ulist,
                                            const uint8_t *pw, const float *bm, float nm, uint16_t *vbuf, int h0,
-                                           int hstep, int hend, int hbase, int HG) {
-    for (int h = h0; h < hend; h += hstep) wave_head_one<T, BLANK>(a, b, n0, U, ulist, pw, bm, nm, vbuf, h, hbase, HG);
+                                           int hstep, int hend, int hbase, int HG, int qlo, int qhi) {
+    for (int h = h0; h < hend; h += hstep)
+        wave_head_one<T, BLANK>(a, b, n0, U, ulist, pw, bm, nm, vbuf, h, hbase, HG, nullptr, qlo, qhi);
 }
 
 // The output projection fused into the wave kernel's epilogue (ClusterAttention's
@@ -604,9 +605,16 @@ __global__ __launch_bounds__(THREADS, 4) void nbhd_attn_wave_kernel(const aff_nb
     const int b = tile / tiles;
     const int n0 = (tile % tiles) * TQ;
     const int n = n0 + q;
-    const bool qlive = n < N;
     const int nc = min(n, N - 1);
     const int nr = (M + LPQ - 1) / LPQ;  // entries per set-up lane that exist (uniform)
+
+    // One pass over the tile's queries [qlo, qhi); the other queries act as dead rows (no
+    // entries, nothing stored).  With split set, a pass whose union is wider than UMAX
+    // (the tile not flagged otherwise) stores nothing and returns true: the caller then
+    // runs the two 16-query halves, each with the union of its own rows, instead of the
+    // per-row routine for all 32 (a half still too wide runs the per-row routine).
+    auto run = [&](const int qlo, const int qhi, const bool split) __attribute__((always_inline)) -> bool {
+    const bool qlive = n < N && q >= qlo && q < qhi;
 
     if (t < 4) red[t] = 0;
     // Table bias modes write the bias store only after the slots step, so their union flags
@@ -832,6 +840,7 @@ __global__ __launch_bounds__(THREADS, 4) void nbhd_attn_wave_kernel(const aff_nb
     }
     lds_barrier();
     const int U = red[2];
+    if (!PROJ && split && !flagged && U > UMAX) return true;
     bool fallback = flagged || U > UMAX;
 
     // ---- union slots; pw codes (plain stores: a code is unique to its (query, neighbour)
@@ -868,11 +877,12 @@ __global__ __launch_bounds__(THREADS, 4) void nbhd_attn_wave_kernel(const aff_nb
 
     if constexpr (!PROJ) {
         if (fallback) {
-            tile_rows<T, BIAS>(a, b, n0, TQ, hb, hn);
-            return;
+            tile_rows<T, BIAS>(a, b, n0 + qlo, qhi - qlo, hb, hn);
+            return false;
         }
         // ---- head phase: wave w, heads hb + w, hb + w + NW, ... of the group
-        wave_heads<T, BLANK>(a, b, n0, U, ulist, pw, bm, nmq_s[lane & 31], sh.vb[w], hb + w, NW, hb + hn, hb, HG);
+        wave_heads<T, BLANK>(a, b, n0, U, ulist, pw, bm, nmq_s[lane & 31], sh.vb[w], hb + w, NW, hb + hn, hb, HG, qlo,
+                             qhi);
     } else {
         // every head of the image in this workgroup, at most one per wave (host-checked);
         // the [32][C] output block is staged in bm's space once every wave is past it
@@ -909,6 +919,15 @@ __global__ __launch_bounds__(THREADS, 4) void nbhd_attn_wave_kernel(const aff_nb
             __syncthreads();
         }
         proj_epilogue<T>(a, pj, b, n0, otile, op, C);
+    }
+    return false;
+    };
+
+    if (run(0, TQ, !PROJ)) {
+        __syncthreads();  // every wave is past the full pass's LDS
+        run(0, TQ / 2, false);
+        __syncthreads();
+        run(TQ / 2, TQ, false);
     }
 }
 

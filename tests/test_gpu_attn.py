@@ -327,3 +327,21 @@ def test_cluster_attention_module_bf16(oracle_mod, dev):
     assert out.dtype == torch.bfloat16
     err = float((out.float() - ref.float()).abs().max())
     assert err <= LOWP_ABS, f"abs err {err:.3e}"
+
+
+def test_cfg2_raster_order_bf16(oracle_mod, dev):
+    """The benchmark shape on raster-ordered tokens: most 32-query tiles have a neighbour
+    union wider than the kernel's 224 slots and run as two 16-query halves (or, if a half
+    is still too wide, the per-row routine)."""
+    w = workloads.cfg2(B=2, order="raster")
+    pos = w["pos"].to(dev)
+    idx = knn(pos, pos, 48)
+    table = (pre_table_fp32.double() @ w["pos_w"].double().T + w["pos_b"].double()).float()
+    out, lse = nbhd_attn_fwd(w["q"].to(dev), w["k"].to(dev), w["v"].to(dev), idx, 32 ** -0.5,
+                             pos=pos, pe_table=table.to(dev), blank_k=w["blank_k"].to(dev),
+                             blank_v=w["blank_v"].to(dev))
+    pe = pe_index(pos, idx)
+    dense = table[pe.cpu()].permute(0, 3, 1, 2).contiguous().numpy()
+    ro, rl = oracle_mod.nbhd_attn(_np(w["q"]), _np(w["k"]), _np(w["v"]), idx.cpu().numpy(), 32 ** -0.5,
+                                  bias=dense, blank_k=_np(w["blank_k"]), blank_v=_np(w["blank_v"]))
+    _assert_lowp(out, lse, ro, rl)
