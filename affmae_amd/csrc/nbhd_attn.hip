@@ -252,7 +252,7 @@ template <> struct Mfma32<f16_t> {
 namespace wt {
 constexpr int TQ = 32;            // queries per workgroup (the MFMA N dimension)
 constexpr int HD = 32;            // head_dim
-constexpr int UMAX = 224;         // union rows: 7 chunks of 32
+constexpr int UMAX = 224;         // union rows: 7 chunks of 32 (a 16-query half tile: 2 UMAX)
 constexpr int WWORDS = 256;       // index-window bitmap words: windows up to 8192 indices
 constexpr int MAXM = 64;          // neighbours per query
 constexpr int LPQ = 8;            // set-up lanes per query
@@ -267,6 +267,7 @@ constexpr float LOG2E = 1.4426950408889634f;
 static_assert(WWORDS == THREADS, "one bitmap word per thread");
 static_assert(TQ * LPQ == THREADS, "one set-up lane group per query");
 static_assert((TQ * PWP) % 16 == 0 && PWP % 4 == 0, "pw is cleared in 16-byte pieces, read in 4-byte ones");
+static_assert(2 * UMAX + 4 <= 2 * PWP, "a half tile's code rows hold 2 UMAX slots");
 static_assert(MAXM + 1 < 256, "a code is an entry number + 1 in 8 bits");
 static_assert(TQ * (NW * HD + 8) * 2 <= BMW * 4, "the projection's output block fits in the bias store");
 }  // namespace wt
@@ -315,7 +316,8 @@ __device__ __forceinline__ void tile_rows(const aff_nbhd_attn_args &a, int b, in
 template <typename T, bool BLANK, bool STAGE = false>
 __device__ __forceinline__ void wave_head_one(const aff_nbhd_attn_args &a, int b, int n0, int U, const int *ulist,
                                               const uint8_t *pw, const float *bm, float nm, uint16_t *vbuf, int h,
-                                              int hbase, int HG, float *yo = nullptr, int qlo = 0, int qhi = wt::TQ) {
+                                              int hbase, int HG, float *yo = nullptr, int qlo = 0, int qhi = wt::TQ,
+                                              int pitch = wt::PWP) {
     using namespace wt;
     using MM = Mfma32<T>;
     const int lane = threadIdx.x & 63;
@@ -332,7 +334,8 @@ __device__ __forceinline__ void wave_head_one(const aff_nbhd_attn_args &a, int b
     const float scale2 = a.scale * LOG2E;
     // transposing-read role: 16-lane group g reads channels 16 (g & 1) + (lane & 15)
     const int kk = (lane & 15) >> 2, aa = lane & 3, cg = 16 * ((lane >> 4) & 1);
-    const uint8_t *pwrow = pw + ql * PWP + 4 * hh;
+    // code rows: one per query of [qlo, qhi), `pitch` bytes apart (other lanes read row 0)
+    const uint8_t *pwrow = pw + (ql >= qlo && ql < qhi ? ql - qlo : 0) * pitch + 4 * hh;
     // V rows go through a 16-row buffer: rows 0..15 of the chunk, then rows 16..31
     const uint32_t vst0 = (lane >> 2) * VRP + (lane & 3) * 8;
     const uint16_t *vtr = vbuf + (4 * hh + kk) * VRP + cg + 4 * aa;
@@ -521,9 +524,9 @@ __device__ __forceinline__ void wave_head_one(const aff_nbhd_attn_args &a, int b
 template <typename T, bool BLANK>
 __device__ __forceinline__ void wave_heads(const aff_nbhd_attn_args &a, int b, int n0, int U, const int *ulist,
                                            const uint8_t *pw, const float *bm, float nm, uint16_t *vbuf, int h0,
-                                           int hstep, int hend, int hbase, int HG, int qlo, int qhi) {
+                                           int hstep, int hend, int hbase, int HG, int qlo, int qhi, int pitch) {
     for (int h = h0; h < hend; h += hstep)
-        wave_head_one<T, BLANK>(a, b, n0, U, ulist, pw, bm, nm, vbuf, h, hbase, HG, nullptr, qlo, qhi);
+        wave_head_one<T, BLANK>(a, b, n0, U, ulist, pw, bm, nm, vbuf, h, hbase, HG, nullptr, qlo, qhi, pitch);
 }
 
 // The output projection fused into the wave kernel's epilogue (ClusterAttention's
@@ -581,7 +584,7 @@ __global__ __launch_bounds__(THREADS, 4) void nbhd_attn_wave_kernel(const aff_nb
     // of each (head, query) -inf, entry 1 + j neighbour j.  The LDS of a workgroup stays under
     // 40 KB, so that four fit on a CU.
     __shared__ __align__(16) float bm[BMW];
-    __shared__ int ulist[UMAX];
+    __shared__ int ulist[2 * UMAX];
     struct SetupLds {
         uint32_t bits[WWORDS];  // one bit per index of the window: a neighbour row
         uint32_t pref[WWORDS];  // union slots before each word
@@ -611,10 +614,12 @@ __global__ __launch_bounds__(THREADS, 4) void nbhd_attn_wave_kernel(const aff_nb
     // One pass over the tile's queries [qlo, qhi); the other queries act as dead rows (no
     // entries, nothing stored).  With split set, a pass whose union is wider than UMAX
     // (the tile not flagged otherwise) stores nothing and returns true: the caller then
-    // runs the two 16-query halves, each with the union of its own rows, instead of the
-    // per-row routine for all 32 (a half still too wide runs the per-row routine).
+    // runs the two 16-query halves, each with the union of its own rows (up to 2 UMAX: its
+    // 16 code rows take the 32 rows' space at twice the pitch), instead of the per-row
+    // routine for all 32 (a half still wider runs the per-row routine).
     auto run = [&](const int qlo, const int qhi, const bool split) __attribute__((always_inline)) -> bool {
-    const bool qlive = n < N && q >= qlo && q < qhi;
+    const bool mine = q >= qlo && q < qhi;  // this lane's query belongs to the pass
+    const bool qlive = n < N && mine;
 
     if (t < 4) red[t] = 0;
     // Table bias modes write the bias store only after the slots step, so their union flags
@@ -841,13 +846,16 @@ __global__ __launch_bounds__(THREADS, 4) void nbhd_attn_wave_kernel(const aff_nb
     lds_barrier();
     const int U = red[2];
     if (!PROJ && split && !flagged && U > UMAX) return true;
-    bool fallback = flagged || U > UMAX;
+    // a half tile's 16 code rows take the 32 rows' space at twice the pitch: 2 UMAX slots
+    const bool half = qhi - qlo == TQ / 2;
+    const int pitch = half ? 2 * PWP : PWP;
+    bool fallback = flagged || U > (half ? 2 * UMAX : UMAX);
 
     // ---- union slots; pw codes (plain stores: a code is unique to its (query, neighbour)
     // entry, so a repeated index within one query shows up as an overwritten code)
     int slot[RJ];
     if (!fallback) {
-        const int rowq = q * PWP;
+        const int rowq = (mine ? q - qlo : 0) * pitch;
 #pragma unroll
         for (int r = 0; r < RJ; ++r) {
             slot[r] = 0;
@@ -865,7 +873,7 @@ __global__ __launch_bounds__(THREADS, 4) void nbhd_attn_wave_kernel(const aff_nb
     lds_barrier();
     if (!fallback) {
         bool dup = false;
-        const int rowq = q * PWP;
+        const int rowq = (mine ? q - qlo : 0) * pitch;
 #pragma unroll
         for (int r = 0; r < RJ; ++r)
             if (r < nr && use[r])
@@ -882,7 +890,7 @@ __global__ __launch_bounds__(THREADS, 4) void nbhd_attn_wave_kernel(const aff_nb
         }
         // ---- head phase: wave w, heads hb + w, hb + w + NW, ... of the group
         wave_heads<T, BLANK>(a, b, n0, U, ulist, pw, bm, nmq_s[lane & 31], sh.vb[w], hb + w, NW, hb + hn, hb, HG, qlo,
-                             qhi);
+                             qhi, pitch);
     } else {
         // every head of the image in this workgroup, at most one per wave (host-checked);
         // the [32][C] output block is staged in bm's space once every wave is past it
