@@ -596,9 +596,7 @@ __global__ __launch_bounds__(THREADS, 4) void nbhd_attn_wave_kernel(const aff_nb
     __shared__ float nmq_s[TQ];
     __shared__ int red[4];  // 0 flagged, 1 repeated index, 2 U
 
-    const int t = threadIdx.x, lane = t & 63;
-    const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: heads index scalar buffers
-    const int q = t >> 3, jl = t & 7;
+    const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);  // wave-uniform: heads index scalar buffers
     const int N = a.N, M = a.M, H = a.H;
     const int tiles = (N + TQ - 1) / TQ;
     // workgroup = (tile, head group): the groups of one tile are adjacent, so on one XCD
@@ -607,8 +605,6 @@ __global__ __launch_bounds__(THREADS, 4) void nbhd_attn_wave_kernel(const aff_nb
     const int tile = wg / ngroups, hb = (wg % ngroups) * HG, hn = min(HG, H - hb);
     const int b = tile / tiles;
     const int n0 = (tile % tiles) * TQ;
-    const int n = n0 + q;
-    const int nc = min(n, N - 1);
     const int nr = (M + LPQ - 1) / LPQ;  // entries per set-up lane that exist (uniform)
 
     // One pass over the tile's queries [qlo, qhi); the other queries act as dead rows (no
@@ -618,6 +614,13 @@ __global__ __launch_bounds__(THREADS, 4) void nbhd_attn_wave_kernel(const aff_nb
     // 16 code rows take the 32 rows' space at twice the pitch), instead of the per-row
     // routine for all 32 (a half still wider runs the per-row routine).
     auto run = [&](const int qlo, const int qhi, const bool split) __attribute__((always_inline)) -> bool {
+    // The lane's indices come from an opaque copy of the thread index in every pass, so
+    // that the compiler recomputes their addresses instead of keeping one pass's values
+    // live (spilled) into the next.
+    int t = int(threadIdx.x);
+    asm volatile("" : "+v"(t));
+    const int lane = t & 63, q = t >> 3, jl = t & 7;
+    const int n = n0 + q, nc = min(n, N - 1);
     const bool mine = q >= qlo && q < qhi;  // this lane's query belongs to the pass
     const bool qlive = n < N && mine;
 
