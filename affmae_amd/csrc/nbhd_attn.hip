@@ -233,12 +233,6 @@ template <> struct Mfma32<bf16_t> {
         return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, b2));
     }
     __device__ __forceinline__ static float to_f32(uint16_t x) { return bf16_to_f32(x); }
-    // acc + lo + hi of a packed pair: one v_dot2c_f32_bf16 against (1, 1)
-    __device__ __forceinline__ static float sum2(uint32_t p, float acc) {
-        typedef __bf16 b2 __attribute__((ext_vector_type(2)));
-        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, p), __builtin_bit_cast(b2, 0x3F803F80u), acc,
-                                               false);
-    }
 };
 template <> struct Mfma32<f16_t> {
     typedef _Float16 v8 __attribute__((ext_vector_type(8)));
@@ -253,11 +247,6 @@ template <> struct Mfma32<f16_t> {
         return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, h2));
     }
     __device__ __forceinline__ static float to_f32(uint16_t x) { return float(__builtin_bit_cast(_Float16, x)); }
-    // acc + lo + hi of a packed pair: one v_dot2c_f32_f16 against (1, 1)
-    __device__ __forceinline__ static float sum2(uint32_t p, float acc) {
-        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-        return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, p), __builtin_bit_cast(h2, 0x3C003C00u), acc, false);
-    }
 };
 
 namespace wt {
@@ -461,27 +450,19 @@ __device__ __forceinline__ void wave_head_one(const aff_nbhd_attn_args &a, int b
 #pragma unroll
                 for (int r = 0; r < 16; ++r) O[r] *= alpha;
             }
-#pragma unroll
-            for (int r = 0; r < 16; ++r) x[r] = __builtin_amdgcn_exp2f(x[r] - m);
-            uint4 pb[2];
-#pragma unroll
-            for (int mm = 0; mm < 2; ++mm)
-                pb[mm] = make_uint4(MM::pack2(x[8 * mm + 0], x[8 * mm + 1]), MM::pack2(x[8 * mm + 2], x[8 * mm + 3]),
-                                    MM::pack2(x[8 * mm + 4], x[8 * mm + 5]), MM::pack2(x[8 * mm + 6], x[8 * mm + 7]));
-            // the denominator sums the 16-bit probabilities that the PV product weights
-            // (two per dot2 instruction)
             float ps = 0.f;
 #pragma unroll
-            for (int mm = 0; mm < 2; ++mm) {
-                ps = MM::sum2(pb[mm].x, ps);
-                ps = MM::sum2(pb[mm].y, ps);
-                ps = MM::sum2(pb[mm].z, ps);
-                ps = MM::sum2(pb[mm].w, ps);
+            for (int r = 0; r < 16; ++r) {
+                x[r] = __builtin_amdgcn_exp2f(x[r] - m);
+                ps += x[r];
             }
             lp += ps;
 #pragma unroll
-            for (int mm = 0; mm < 2; ++mm)
-                O = MM::mma(make_uint4(vt[2 * mm].x, vt[2 * mm].y, vt[2 * mm + 1].x, vt[2 * mm + 1].y), pb[mm], O);
+            for (int mm = 0; mm < 2; ++mm) {
+                const uint4 pb = make_uint4(MM::pack2(x[8 * mm + 0], x[8 * mm + 1]), MM::pack2(x[8 * mm + 2], x[8 * mm + 3]),
+                                            MM::pack2(x[8 * mm + 4], x[8 * mm + 5]), MM::pack2(x[8 * mm + 6], x[8 * mm + 7]));
+                O = MM::mma(make_uint4(vt[2 * mm].x, vt[2 * mm].y, vt[2 * mm + 1].x, vt[2 * mm + 1].y), pb, O);
+            }
         };
 
         // The fetches are unconditional (past the last chunk they re-read it): a
@@ -708,9 +689,7 @@ __global__ __launch_bounds__(THREADS, 4) void nbhd_attn_wave_kernel(const aff_nb
     // once; mode 0 stores zeros.
     const int PL = TQ * (M + 1);             // bm words per head plane
     const int rowq_b = q * (M + 1) + 1;      // bm word of (q, j = 0) in head 0's plane
-    // fp32 table of 4-head rows, read with 32-bit byte offsets
-    const bool fast4 = (BIAS == 2 || BIAS == 4) && HG == 4 && H % 4 == 0 && a.table_dtype == AFF_F32 &&
-                       a.table_rows * H < ((int64_t)1 << 29);
+    const bool fast4 = (BIAS == 2 || BIAS == 4) && HG == 4 && H % 4 == 0 && a.table_dtype == AFF_F32;
     float2 gq[RJ];   // BIAS 4: neighbour coordinates
     int64_t prow[RJ];  // BIAS 2: pe rows
     float pqx = 0.f, pqy = 0.f;
@@ -761,36 +740,21 @@ __global__ __launch_bounds__(THREADS, 4) void nbhd_attn_wave_kernel(const aff_nb
         else return pe_from_coords32(pqx, pqy, gq[r].x, gq[r].y, float(a.rel_width), float(Tw));
     };
     // fp32 table, 4 heads: one 16-byte row per entry, loaded after the bits step and
-    // stored to bm after the slots step.  Branch-free: every entry of the lane loads (an
-    // unused entry or a row outside the table takes row 0 and a zero scale) through a
-    // buffer resource sized to the table, at 32-bit offsets.
+    // stored to bm after the slots step
     float4 tv[RJ];
     float tsc[RJ];
     auto load_table_rows = [&]() {
         if constexpr (BIAS == 2 || BIAS == 4) {
             if (fast4) {
-                const auto rt = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.table), (short)0,
-                                                                  int(a.table_rows * H * 4), 0x00020000);
-                const uint32_t tstride = uint32_t(H) * 4u, tbase = uint32_t(hb) * 4u;
-                const uint32_t trows = uint32_t(a.table_rows);
-                float qxw = 0.f, qyw = 0.f;
-                const float W2 = 2.f * float(a.rel_width);
-                if constexpr (BIAS == 4) {
-                    qxw = pqx - float(a.rel_width);
-                    qyw = pqy - float(a.rel_width);
-                }
 #pragma unroll
                 for (int r = 0; r < RJ; ++r) {
                     tv[r] = make_float4(0.f, 0.f, 0.f, 0.f);
                     tsc[r] = 0.f;
-                    if (r >= nr) continue;  // uniform
-                    uint32_t row;
-                    if constexpr (BIAS == 4) row = uint32_t(pe_from_rel32(qxw, qyw, gq[r].x, gq[r].y, W2, float(Tw)));
-                    else row = prow[r] >= 0 && prow[r] < (int64_t)trows ? uint32_t(prow[r]) : trows;
-                    const bool in = use[r] && row < trows;
+                    if (r >= nr || !use[r]) continue;
+                    const int64_t row = table_row(r);
+                    const bool in = row >= 0 && row < a.table_rows;
                     tsc[r] = in ? LOG2E : 0.f;
-                    tv[r] = __builtin_bit_cast(
-                        float4, __builtin_amdgcn_raw_buffer_load_b128(rt, int((in ? row : 0u) * tstride + tbase), 0, 0));
+                    tv[r] = reinterpret_cast<const float4 *>(a.table)[((in ? row : 0) * H + hb) >> 2];
                 }
             }
         }

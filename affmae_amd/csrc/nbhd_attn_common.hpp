@@ -34,15 +34,6 @@ __device__ __forceinline__ int pe_from_coords32(float qx, float qy, float mx, fl
     return int(ry * T + rx);
 }
 
-// pe_from_coords32 with the query's terms precomputed once for all its neighbours:
-// qxw = qx - W, qyw = qy - W, W2 = 2 W (the same operations, so the same row).
-__device__ __forceinline__ int pe_from_rel32(float qxw, float qyw, float mx, float my, float W2, float T) {
-#pragma clang fp contract(off)
-    const float rx = fminf(fmaxf(mx - qxw, 0.f), W2);
-    const float ry = fminf(fmaxf(my - qyw, 0.f), W2);
-    return int(ry * T + rx);
-}
-
 // Continuous relative-position features f(dx, dy) = (dx, dy, r, dy/r, dx/r).
 __device__ __forceinline__ float cont_bias(const float *pw, float pb, float dx, float dy) {
     const float r = sqrtf(dx * dx + dy * dy);
