@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import concurrent.futures as cf
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -50,12 +51,42 @@ EXTRA_FLAGS = {
 }
 
 
+# Hot kernels that must compile without scratch (register spills): a spill in the
+# attention kernel once added 18.8 MB of HBM writes per launch.  The compiler's
+# resource-usage remarks are checked for every kernel whose name contains the string.
+NO_SCRATCH = {
+    "nbhd_attn.hip": "nbhd_attn_wave_kernel",
+    "knn.hip": "knn_win_kernel",
+}
+
+
+def _scratch_kernels(remarks: str, name_part: str) -> list:
+    """(kernel, bytes per lane) of every kernel containing name_part with scratch > 0."""
+    bad, cur = [], None
+    for line in remarks.splitlines():
+        m = re.search(r"remark: Function Name: (\S+)", line)
+        if m:
+            cur = m.group(1)
+            continue
+        m = re.search(r"remark:\s+ScratchSize \[bytes/lane\]: (\d+)", line)
+        if m and cur and name_part in cur and int(m.group(1)) > 0:
+            bad.append((cur, int(m.group(1))))
+    return bad
+
+
 def _compile(src: Path) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [HIPCC, *COMMON_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
+    check = NO_SCRATCH.get(src.name)
+    remarks = ["-Rpass-analysis=kernel-resource-usage"] if check else []
+    cmd = [HIPCC, *COMMON_FLAGS, *EXTRA_FLAGS.get(src.name, []), *remarks, "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
+    if check:
+        bad = _scratch_kernels(proc.stderr, check)
+        if bad:
+            raise RuntimeError(f"{src.name}: kernels compiled with scratch (register spills): " +
+                               ", ".join(f"{k} {n} B/lane" for k, n in bad[:4]))
     return obj
 
 
